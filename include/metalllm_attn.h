@@ -1,0 +1,90 @@
+/* metalllm_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in for the three Metal kernels of metalLLM's attention layer:
+ *   flashAttentionForward  /root/reference/attention.metal:56-164, dispatched at
+ *                          /root/reference/model.h:459-473
+ *   computeD               /root/reference/attention.metal:166-195, model.h:639-647
+ *   flashAttentionBackward /root/reference/attention.metal:198-299, model.h:648-665
+ * Arguments keep the reference's buffer-index order (q0 k1 v2 out3 l4 params5; dO0 O1 D2 params3;
+ * dZ0 d1 l2 q3 k4 v5 dQ6 dK7 dV8 params9) with a HIP stream appended.
+ *
+ * Layouts (all row-major, caller-owned device memory, 16-byte aligned):
+ *   q, k, v, out, dO, dK, dV : bf16 bit patterns, [B, T, NH, D] (one token row = N = NH*D elements;
+ *                              for B = 1 this is the reference's [T, N] buffer)
+ *   l (logsumexp), D         : fp32 [B, NH, T] (the reference indexes them [t*NH + h], one sequence)
+ *   dQ                       : fp32 [B, T, NH, D], ACCUMULATED into with atomics: the caller zeroes
+ *                              it first, as model.h:549 does
+ * dK and dV are written in full (the reference accumulates into caller-zeroed buffers,
+ * model.h:550-551; the result is the same). D holds the bf16-rounded value of rowsum(dO*O),
+ * stored as fp32.
+ *
+ * Semantics: asynchronous on `stream` (NULL = the default stream); no allocation, no host
+ * synchronisation, no global state, so calls on distinct streams may run concurrently. Each
+ * entry point validates its arguments before touching the device and returns METALLLM_ATTN_OK or
+ * a negative error code; a failed kernel launch returns METALLLM_ATTN_E_LAUNCH.
+ * Supported shapes: M (= T) a positive multiple of 64, D in {64, 128}, N == NH*D, B >= 1,
+ * B*M*N < 2^31 elements per tensor.
+ */
+#ifndef METALLLM_ATTN_H
+#define METALLLM_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* metalllm_stream_t; /* same type as hipStream_t */
+
+/* attention.metal:7-12 / main.cpp:114-119: {M, N, D, NH}; B is appended (the reference runs
+ * one sequence). */
+typedef struct AttentionParams {
+  uint32_t M;  /* sequence length T */
+  uint32_t N;  /* NH * D */
+  uint32_t D;  /* head size, 64 or 128 */
+  uint32_t NH; /* number of heads */
+  uint32_t B;  /* batch */
+} AttentionParams;
+
+enum {
+  METALLLM_ATTN_OK = 0,
+  METALLLM_ATTN_E_NULL = -1,     /* a required pointer is NULL */
+  METALLLM_ATTN_E_SEQLEN = -2,   /* M == 0 or M % 64 != 0 */
+  METALLLM_ATTN_E_HEADDIM = -3,  /* D not in {64, 128} */
+  METALLLM_ATTN_E_LAYOUT = -4,   /* N != NH * D, NH == 0 or B == 0 */
+  METALLLM_ATTN_E_SIZE = -5,     /* a tensor exceeds 2^31 elements */
+  METALLLM_ATTN_E_ALIGN = -6,    /* a tensor pointer is not 16-byte aligned */
+  METALLLM_ATTN_E_LAUNCH = -7    /* the kernel launch failed */
+};
+
+/* Replaces the flashAttentionForward dispatch at model.h:459-473 (attention.metal:56-164).
+ * out = softmax(q k^T / sqrt(D) + causal mask) v per (b, head); l = logsumexp per query row. */
+int flashAttentionForward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* l,
+                          const AttentionParams* p, metalllm_stream_t stream);
+
+/* Replaces the computeD dispatch at model.h:639-647 (attention.metal:166-195).
+ * D[b,h,t] = bf16( sum_d bf16(dO*O) ). */
+int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionParams* p,
+             metalllm_stream_t stream);
+
+/* Replaces the flashAttentionBackward dispatch at model.h:648-665 (attention.metal:198-299).
+ * dZ is dO; d and l are computeD's and the forward's outputs. dQ += gradient (fp32 atomics);
+ * dK, dV = gradients (bf16). */
+int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                           const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                           const AttentionParams* p, metalllm_stream_t stream);
+
+/* Static description of an error code (no counterpart in the reference, which has no error
+ * path per kernel; model.h:333-336,361-365 only print). */
+const char* metalllmAttnErrorString(int code);
+
+/* Test hook (no counterpart in the reference): writes, for workgroup ids 0..count-1 of the
+ * forward (kind 0) or backward (kind 1) grid of shape p, the (pair, block) each one owns into
+ * out[2*i], out[2*i+1]. Returns the grid size, or a negative error code. Host-only. */
+int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_t count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* METALLLM_ATTN_H */

@@ -1,0 +1,10 @@
+"""metalllm_amd: MI355X (gfx950) attention hot path of metalLLM.
+
+The product is libmetalllm_attn.so (C ABI in include/metalllm_attn.h); this package builds it
+(`metalllm_amd.build`) and binds it (`metalllm_amd.attention`).
+"""
+from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, computeD,
+                        flashAttentionBackward, flashAttentionForward, library, work_map)
+
+__all__ = ["AttentionError", "AttentionParams", "attention_backward", "attention_forward", "computeD",
+           "flashAttentionBackward", "flashAttentionForward", "library", "work_map"]

@@ -1,0 +1,49 @@
+"""Builds libmetalllm_attn.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+
+    python -m metalllm_amd.build          # compile
+    python -m metalllm_amd.build --stats  # also print register / LDS use per kernel
+
+hipcc cross-compiles for gfx950 without a GPU. The packed-fp32 target feature is disabled on
+purpose: every fp32 op stays scalar (v_pk_* fp32 forms are not used on this platform).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libmetalllm_attn.so")
+SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_computed.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off",            # keep the reference's separate multiply/add roundings
+    "-munsafe-fp-atomics",          # hardware global_atomic_add_f32 for the dQ accumulator
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+]
+
+
+def build(stats: bool = False, verbose: bool = False) -> str:
+    cmd = [HIPCC, *FLAGS]
+    if stats:
+        cmd += ["-Rpass-analysis=kernel-resource-usage"]
+    cmd += [os.path.join(CSRC, s) for s in SOURCES] + ["-o", LIB + ".tmp"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "unknown target feature"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    os.replace(LIB + ".tmp", LIB)
+    if stats or verbose:
+        print(err)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(stats="--stats" in sys.argv, verbose=True)
+    print("built", LIB)

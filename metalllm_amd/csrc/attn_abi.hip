@@ -1,0 +1,95 @@
+// attn_abi.hip -- extern "C" entry points of libmetalllm_attn.so (declared in
+// include/metalllm_attn.h). Validation happens on the host before any HIP call, so argument
+// errors are reported without touching the device.
+#include <cmath>
+#include "../../include/metalllm_attn.h"
+#include "attn_launch.hpp"
+
+namespace {
+
+int validate(const AttentionParams* p) {
+  if (!p) return METALLLM_ATTN_E_NULL;
+  if (p->M == 0 || p->M % 64) return METALLLM_ATTN_E_SEQLEN;
+  if (p->D != 64 && p->D != 128) return METALLLM_ATTN_E_HEADDIM;
+  if (p->NH == 0 || p->B == 0 || (uint64_t)p->N != (uint64_t)p->NH * p->D) return METALLLM_ATTN_E_LAYOUT;
+  if ((uint64_t)p->B * p->M * p->N >= (1ull << 31)) return METALLLM_ATTN_E_SIZE;
+  return METALLLM_ATTN_OK;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+float head_scale(uint32_t D) { return 1.0f / std::sqrt((float)D); }  // attention.metal:109,268
+
+}  // namespace
+
+extern "C" {
+
+int flashAttentionForward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* l,
+                          const AttentionParams* p, metalllm_stream_t stream) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (!q || !k || !v || !out || !l) return METALLLM_ATTN_E_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(l))
+    return METALLLM_ATTN_E_ALIGN;
+  mla::FwdArgs a{q, k, v, out, l, (int)p->M, (int)p->NH, (int)p->B, head_scale(p->D)};
+  return mla::launch_forward(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                               : METALLLM_ATTN_E_LAUNCH;
+}
+
+int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionParams* p, metalllm_stream_t stream) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (!dO || !O || !D) return METALLLM_ATTN_E_NULL;
+  if (!aligned16(dO) || !aligned16(O) || !aligned16(D)) return METALLLM_ATTN_E_ALIGN;
+  mla::ComputeDArgs a{dO, O, D, (int)p->M, (int)p->NH, (int)p->B};
+  return mla::launch_compute_d(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                                : METALLLM_ATTN_E_LAUNCH;
+}
+
+int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                           const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                           const AttentionParams* p, metalllm_stream_t stream) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
+  if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
+    return METALLLM_ATTN_E_ALIGN;
+  mla::BwdArgs a{dZ, d, l, q, k, v, dQ, dK, dV, (int)p->M, (int)p->NH, (int)p->B, head_scale(p->D)};
+  return mla::launch_backward(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                               : METALLLM_ATTN_E_LAUNCH;
+}
+
+const char* metalllmAttnErrorString(int code) {
+  switch (code) {
+    case METALLLM_ATTN_OK: return "ok";
+    case METALLLM_ATTN_E_NULL: return "a required pointer is NULL";
+    case METALLLM_ATTN_E_SEQLEN: return "sequence length M must be a positive multiple of 64";
+    case METALLLM_ATTN_E_HEADDIM: return "head size D must be 64 or 128";
+    case METALLLM_ATTN_E_LAYOUT: return "N must equal NH*D with NH >= 1 and B >= 1";
+    case METALLLM_ATTN_E_SIZE: return "a tensor exceeds 2^31 elements";
+    case METALLLM_ATTN_E_ALIGN: return "tensor pointers must be 16-byte aligned";
+    case METALLLM_ATTN_E_LAUNCH: return "kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_t count) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (!out && count > 0) return METALLLM_ATTN_E_NULL;
+  if (kind != 0 && kind != 1) return METALLLM_ATTN_E_LAYOUT;
+  const int npairs = (int)(p->B * p->NH);
+  const int blk = kind == 0 ? mla::kFwdBlockM : mla::kBwdBlockN;
+  const int nblk = ((int)p->M + blk - 1) / blk;
+  const int grid = npairs * nblk;
+  for (int i = 0; i < count && i < grid; ++i) {
+    int pair, b;
+    mla::decode_workgroup(i, npairs, nblk, kind == 0, pair, b);
+    out[2 * i] = pair;
+    out[2 * i + 1] = b;
+  }
+  return grid;
+}
+
+}  // extern "C"

@@ -1,0 +1,68 @@
+// attn_launch.hpp -- host-side launch interface between the C ABI (attn_abi.hip) and the
+// kernels (attn_fwd.hip, attn_bwd.hip, attn_computed.hip). Shapes arrive validated.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mla {
+
+// Q/K/V/O/dO/dQ/dK/dV are [B,T,H,D] (row of one token = H*D elements); LSE and D are [B,H,T].
+struct FwdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;
+  float* lse;
+  int T, H, B;
+  float scale;  // 1/sqrt(D) in fp32, as the reference computes it (attention.metal:109)
+};
+
+struct ComputeDArgs {
+  const uint16_t* dO;
+  const uint16_t* O;
+  float* Dv;
+  int T, H, B;
+};
+
+struct BwdArgs {
+  const uint16_t* dO;
+  const float* Dv;
+  const float* lse;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  float* dQ;
+  uint16_t* dK;
+  uint16_t* dV;
+  int T, H, B;
+  float scale;
+};
+
+hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s);
+hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
+hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);
+
+// Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
+// spread so that every block of one pair lands on the same XCD (workgroups are handed to the
+// 8 XCDs round-robin by id), and blocks are ordered with the largest causal work first.
+//   forward : block = query block, longest (last) first
+//   backward: block = key block, longest (first) first
+__host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, bool last_first, int& pair,
+                                                 int& blk) {
+  int local;
+  if ((npairs & 7) == 0) {
+    const int xcd = bid & 7, slot = bid >> 3;
+    pair = (slot / nblk) * 8 + xcd;
+    local = slot % nblk;
+  } else {
+    pair = bid / nblk;
+    local = bid % nblk;
+  }
+  blk = last_first ? (nblk - 1 - local) : local;
+}
+
+constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
+constexpr int kBwdBlockN = 128;  // keys owned by one backward workgroup
+constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)
+
+}  // namespace mla

@@ -1,0 +1,127 @@
+"""ctypes wrapper of the CPU oracle (liboracle_attn.so, built from oracle/attn_oracle.cpp).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker. The product (metalllm_amd/) never imports this package.
+
+Arrays are numpy: bf16 tensors travel as uint16 bit patterns in [B, T, H, D] layout,
+LSE and D as float32 [B, H, T], dQ as float32 [B, T, H, D] (accumulated into, caller zeroes).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_attn.so")
+
+GEMM_CHUNK16 = 0
+GEMM_SEQ = 1
+GEMM_MFMA = 2
+BWD_REFERENCE = 0
+BWD_FP32 = 1
+
+
+class AttentionParams(ctypes.Structure):
+    _fields_ = [("M", ctypes.c_uint32), ("N", ctypes.c_uint32), ("D", ctypes.c_uint32),
+                ("NH", ctypes.c_uint32), ("B", ctypes.c_uint32)]
+
+
+class OracleOpts(ctypes.Structure):
+    _fields_ = [("threads", ctypes.c_int), ("b_begin", ctypes.c_int), ("b_end", ctypes.c_int),
+                ("gemm_model", ctypes.c_int), ("bwd_mode", ctypes.c_int), ("d_round", ctypes.c_int)]
+
+
+def build(force: bool = False) -> str:
+    """Compiles liboracle_attn.so with oracle/Makefile (gcc only, no GPU needed)."""
+    if force or not os.path.exists(_LIB_PATH):
+        cmd = ["make", "-C", _HERE]
+        if force:
+            cmd.insert(1, "-B")
+        subprocess.run(cmd, check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+        f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+        pp = ctypes.POINTER(AttentionParams)
+        op = ctypes.POINTER(OracleOpts)
+        L.oracle_forward.argtypes = [u16p, u16p, u16p, u16p, f32p, pp, op]
+        L.oracle_compute_d.argtypes = [u16p, u16p, f32p, pp, op]
+        L.oracle_backward.argtypes = [u16p, f32p, f32p, u16p, u16p, u16p, f32p, u16p, u16p, pp, op]
+        L.oracle_fill_normal_bf16.argtypes = [u16p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float]
+        L.oracle_fill_normal_bf16.restype = None
+        _lib = L
+    return _lib
+
+
+def params(B: int, T: int, H: int, D: int) -> AttentionParams:
+    return AttentionParams(T, H * D, D, H, B)
+
+
+def opts(threads: int = 0, b_begin: int = 0, b_end: int = 0, gemm_model: int = GEMM_MFMA,
+         bwd_mode: int = BWD_REFERENCE, d_round: int = 1) -> OracleOpts:
+    return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round)
+
+
+# Tensor ids of the seeded input generator.
+TID_Q, TID_K, TID_V, TID_DO = 1, 2, 3, 4
+
+
+def normal_bf16(shape, seed: int, tensor_id: int, scale: float = 1.0) -> np.ndarray:
+    """Seeded N(0,1)*scale bf16 bits; element i keyed by (seed, tensor_id, flat index i)."""
+    out = np.empty(int(np.prod(shape)), dtype=np.uint16)
+    lib().oracle_fill_normal_bf16(out, out.size, seed, tensor_id, scale)
+    return out.reshape(shape)
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise ValueError(f"oracle {what} rejected the arguments (rc={rc})")
+
+
+def forward(q, k, v, o: OracleOpts | None = None):
+    B, T, H, D = q.shape
+    out = np.zeros_like(q)
+    lse = np.zeros((B, H, T), dtype=np.float32)
+    _check(lib().oracle_forward(q, k, v, out, lse, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())), "forward")
+    return out, lse
+
+
+def compute_d(dO, O, o: OracleOpts | None = None):
+    B, T, H, D = dO.shape
+    Dv = np.zeros((B, H, T), dtype=np.float32)
+    _check(lib().oracle_compute_d(dO, O, Dv, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())), "computeD")
+    return Dv
+
+
+def backward(dO, Dv, lse, q, k, v, o: OracleOpts | None = None):
+    B, T, H, D = q.shape
+    dQ = np.zeros((B, T, H, D), dtype=np.float32)
+    dK = np.zeros_like(q)
+    dV = np.zeros_like(q)
+    _check(lib().oracle_backward(dO, Dv, lse, q, k, v, dQ, dK, dV, ctypes.byref(params(B, T, H, D)),
+                                 ctypes.byref(o or opts())), "backward")
+    return dQ, dK, dV
+
+
+def bf16_to_f32(x: np.ndarray) -> np.ndarray:
+    return (x.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bits (finite values)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)

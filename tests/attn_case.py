@@ -1,0 +1,89 @@
+"""Shared helpers: seeded inputs from the oracle's generator, oracle runs, GPU runs, error metrics."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+
+def make_inputs(B, T, H, D, seed=1, qk_scale=1.0):
+    q = O.normal_bf16((B, T, H, D), seed, O.TID_Q, qk_scale)
+    k = O.normal_bf16((B, T, H, D), seed, O.TID_K, qk_scale)
+    v = O.normal_bf16((B, T, H, D), seed, O.TID_V)
+    g = O.normal_bf16((B, T, H, D), seed, O.TID_DO)
+    return q, k, v, g
+
+
+def oracle_all(q, k, v, g, **kw):
+    o = O.opts(**kw)
+    out, lse = O.forward(q, k, v, o)
+    Dv = O.compute_d(g, out, o)
+    dQ, dK, dV = O.backward(g, Dv, lse, q, k, v, o)
+    return dict(out=out, lse=lse, D=Dv, dQ=dQ, dK=dK, dV=dV)
+
+
+def to_gpu(x, dev):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if x.dtype == np.uint16:
+        t = t.view(torch.bfloat16)
+    return t.to(dev)
+
+
+def to_np(t):
+    import torch
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def gpu_forward(q, k, v, dev):
+    import metalllm_amd as M
+    out, lse = M.attention_forward(to_gpu(q, dev), to_gpu(k, dev), to_gpu(v, dev))
+    return to_np(out), to_np(lse)
+
+
+def gpu_backward(g, Dv, lse, q, k, v, dev):
+    """flashAttentionBackward alone on given D / lse (dQ zeroed first)."""
+    import torch
+    import metalllm_amd as M
+    tq, tk, tv, tg = (to_gpu(x, dev) for x in (q, k, v, g))
+    dQ = torch.zeros(q.shape, dtype=torch.float32, device=dev)
+    dK = torch.empty_like(tq)
+    dV = torch.empty_like(tq)
+    M.flashAttentionBackward(tg, to_gpu(Dv, dev), to_gpu(lse, dev), tq, tk, tv, dQ, dK, dV)
+    return to_np(dQ), to_np(dK), to_np(dV)
+
+
+def gpu_compute_d(g, out, dev):
+    import torch
+    import metalllm_amd as M
+    B, T, H, D = g.shape
+    Dv = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    M.computeD(to_gpu(g, dev), to_gpu(out, dev), Dv)
+    return to_np(Dv)
+
+
+def f32(x):
+    return O.bf16_to_f32(x) if x.dtype == np.uint16 else x.astype(np.float32)
+
+
+def bf16_ulp(x):
+    """Spacing of bf16 values at |x| (normal range)."""
+    ax = np.maximum(np.abs(x), np.float32(2.0 ** -126))
+    e = np.floor(np.log2(ax))
+    return np.exp2(e - 7).astype(np.float32)
+
+
+def out_error(out_gpu, out_ref):
+    """Max abs error of O, and the count of elements beyond max(1e-2, 1 bf16 ulp of the reference)."""
+    a, b = f32(out_gpu), f32(out_ref)
+    d = np.abs(a - b)
+    bar = np.maximum(np.float32(1e-2), bf16_ulp(b))
+    return float(d.max()), int((d > bar).sum()), int((d > 1e-2).sum())
+
+
+def rel_to_max(x, ref):
+    a, b = f32(x), f32(ref)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))

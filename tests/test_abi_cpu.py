@@ -1,0 +1,64 @@
+"""C ABI checks that need no GPU: the library loads, exports what include/metalllm_attn.h declares,
+and rejects invalid arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import metalllm_amd as M
+from metalllm_amd.attention import AttentionParams, EXPORTED
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "metalllm_attn.h")).read()
+    return set(re.findall(r"^(?:int|const char\*)\s+(\w+)\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = M.library()
+    names = declared_functions()
+    assert names == set(EXPORTED)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+BAD = [
+    (dict(M=0), -2), (dict(M=100), -2), (dict(M=65), -2),
+    (dict(D=32), -3), (dict(D=96), -3), (dict(D=256), -3),
+    (dict(N=383), -4), (dict(NH=0, N=0), -4), (dict(B=0), -4),
+    (dict(B=1 << 12, M=1 << 16), -5),
+]
+
+
+@pytest.mark.parametrize("change,code", BAD)
+def test_invalid_shapes_rejected_without_device(change, code):
+    lib = M.library()
+    f = dict(M=256, N=384, D=64, NH=6, B=1)
+    f.update(change)
+    p = AttentionParams(f["M"], f["N"], f["D"], f["NH"], f["B"])
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.flashAttentionForward(fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
+    assert lib.computeD(fake, fake, fake, ctypes.byref(p), None) == code
+    assert lib.flashAttentionBackward(fake, fake, fake, fake, fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
+
+
+def test_null_and_alignment_rejected():
+    lib = M.library()
+    p = AttentionParams(256, 384, 64, 6, 1)
+    ok = ctypes.c_void_p(1 << 20)
+    assert lib.flashAttentionForward(ok, ok, None, ok, ok, ctypes.byref(p), None) == -1
+    assert lib.computeD(ok, None, ok, ctypes.byref(p), None) == -1
+    assert lib.flashAttentionBackward(ok, ok, ok, ok, ok, ok, None, ok, ok, ctypes.byref(p), None) == -1
+    assert lib.flashAttentionForward(ok, ok, ok, ok, ok, None, None) == -1
+    bad = ctypes.c_void_p((1 << 20) + 2)
+    assert lib.flashAttentionForward(ok, ok, bad, ok, ok, ctypes.byref(p), None) == -6
+    assert lib.computeD(ok, ok, bad, ctypes.byref(p), None) == -6
+
+
+def test_error_strings():
+    lib = M.library()
+    for code in range(-7, 1):
+        assert lib.metalllmAttnErrorString(code)
