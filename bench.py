@@ -1,0 +1,196 @@
+"""Benchmark of the causal attention hot path (flashAttentionForward + computeD +
+flashAttentionBackward) on one MI355X, through the C ABI.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+
+One step = dQ zeroing + flashAttentionForward + computeD + flashAttentionBackward over one batch of
+synthetic bf16 inputs already resident in HBM (the reference's per-layer sequence, model.h:459-473,
+549-551, 639-665). Prints ONE JSON line. FLOPs use the causal FlashAttention convention (half of
+dense): fwd 2*B*H*T^2*D, bwd 5*B*H*T^2*D, step 7*B*H*T^2*D.
+
+The roofline object describes the dominant kernel (flashAttentionBackward): its algorithmic FLOPs
+per launch over its average launch time measured with HIP events on the launch stream, against
+MI355X dense bf16 matrix peak. cpu_baseline times the CPU oracle (the scalar C++ transcription
+of the reference math, oracle/attn_oracle.cpp) on a bounded sample of the same workload on this
+host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 matrix peak
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # id: (B, H, T, D, qk_scale, description)
+    1: (128, 6, 256, 64, 1.0, "metalLLM training shape, larger batch"),
+    2: (32, 12, 1024, 64, 1.5, "GPT-2-small-like, Q/K x1.5"),
+    3: (16, 16, 4096, 128, 1.0, "long-context D=128 (target shape)"),
+}
+
+
+def flops(B, H, T, D):
+    base = B * H * T * T * D
+    return 2.0 * base, 5.0 * base
+
+
+def traffic_from_profiles(cfg_id):
+    """HBM bytes per backward launch measured by rocprofv3 --pmc, if a summary was committed."""
+    path = os.path.join(ROOT, "profiles", f"bwd_traffic_config{cfg_id}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def cpu_baseline(B, H, T, D, qk_scale, threads):
+    """Times the oracle (fwd + computeD + bwd) on batch 0 and a bounded number of heads."""
+    import numpy as np
+    import oracle as O
+    heads = min(H, threads)
+    o = O.opts(threads=threads)
+    q = O.normal_bf16((1, T, heads, D), 1, O.TID_Q, qk_scale)
+    k = O.normal_bf16((1, T, heads, D), 1, O.TID_K, qk_scale)
+    v = O.normal_bf16((1, T, heads, D), 1, O.TID_V)
+    g = O.normal_bf16((1, T, heads, D), 1, O.TID_DO)
+    t0 = time.perf_counter()
+    out, lse = O.forward(q, k, v, o)
+    Dv = O.compute_d(g, out, o)
+    O.backward(g, Dv, lse, q, k, v, o)
+    dt = time.perf_counter() - t0
+    ff, fb = flops(1, heads, T, D)
+    return {
+        "value": (ff + fb) / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"b=0, {heads} of {H} heads (T={T}, D={D}): fwd+computeD+bwd of the oracle "
+                  f"(scalar C++ transcription, matrix-core pass model), {dt:.1f} s on {threads} threads; "
+                  f"rate scales to the full batch",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU hot path only: attention shards per (batch, head) with no "
+              "exchange, so this build runs and reports one GPU (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import metalllm_amd as M
+
+    B, H, T, D, qk_scale, desc = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    shape = (B, T, H, D)
+
+    def randn(scale=1.0):
+        return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * scale).to(torch.bfloat16)
+
+    q, k, v, dO = randn(qk_scale), randn(qk_scale), randn(), randn()
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    Dv = torch.empty_like(lse)
+    dQ = torch.empty(shape, dtype=torch.float32, device=dev)
+    dK = torch.empty_like(q)
+    dV = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    p = M.AttentionParams.of(B, T, H, D)
+
+    def step(ev=None):
+        dQ.zero_()
+        if ev is not None:
+            ev[0].record(stream)
+        M.flashAttentionForward(q, k, v, out, lse, stream, p)
+        if ev is not None:
+            ev[1].record(stream)
+        M.computeD(dO, out, Dv, stream, p)
+        if ev is not None:
+            ev[2].record(stream)
+        M.flashAttentionBackward(dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
+        if ev is not None:
+            ev[3].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # per-kernel times from the events (the dQ zeroing is in the step, outside the kernel intervals)
+    fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
+    cd_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
+    bwd_ms = sorted(e[2].elapsed_time(e[3]) for e in events)
+    avg = lambda xs: sum(xs) / len(xs)
+    med = lambda xs: xs[len(xs) // 2]
+    ff, fb = flops(B, H, T, D)
+    ms_per_step = wall * 1e3 / args.steps
+    value = (ff + fb) / (ms_per_step * 1e-3) / 1e12
+    bwd_avg = avg(bwd_ms)
+    achieved = fb / (bwd_avg * 1e-3) / 1e12
+
+    bthd = B * T * H * D
+    result = {
+        "metric": "causal attn fwd+bwd TFLOP/s at B,H,T,D bf16; % of MI355X bf16 MFMA peak",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config{args.config}: causal attention fwd+computeD+bwd, {desc}",
+                   "B": B, "H": H, "T": T, "D": D, "qk_scale": qk_scale, "causal": True},
+        "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "phases": {
+            "fwd_ms_median": round(med(fwd_ms), 4), "computeD_ms_median": round(med(cd_ms), 4),
+            "bwd_ms_median": round(med(bwd_ms), 4),
+            "fwd_tflops": round(ff / (med(fwd_ms) * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(fb / (med(bwd_ms) * 1e-3) / 1e12, 2),
+            "computeD_gbs": round((4 * bthd + 4 * B * H * T) / (med(cd_ms) * 1e-3) / 1e9, 1),
+        },
+        "roofline": {
+            "kernel": "flashAttentionBackward",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic_from_profiles(args.config),
+            "algorithmic_bytes": 16 * bthd + 8 * B * H * T,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(B, H, T, D, qk_scale, args.cpu_threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -28,19 +28,36 @@ FLAGS = [
 ]
 
 
-def build(stats: bool = False, verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS]
-    if stats:
-        cmd += ["-Rpass-analysis=kernel-resource-usage"]
-    cmd += [os.path.join(CSRC, s) for s in SOURCES] + ["-o", LIB + ".tmp"]
+# Per-source extra flags: the backward keeps its matrix-core accumulators in arch VGPRs (they
+# are rounded by VALU code every query block, and AGPR<->VGPR copies would dominate).
+EXTRA = {"attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
+def _run(cmd):
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "unknown target feature"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "packed-fp32-ops" not in l)
+    err = "\n".join(l for l in res.stderr.splitlines()
+                    if "unknown target feature" not in l and "packed-fp32-ops" not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(stats: bool = False, verbose: bool = False) -> str:
+    objs, logs = [], []
+    odir = os.path.join(PKG, "_build")
+    os.makedirs(odir, exist_ok=True)
+    for src in SOURCES:
+        obj = os.path.join(odir, src + ".o")
+        cmd = [HIPCC, *FLAGS, "-c", *EXTRA.get(src, [])]
+        cmd = [c for c in cmd if c != "-shared"]
+        if stats:
+            cmd += ["-Rpass-analysis=kernel-resource-usage"]
+        logs.append(_run(cmd + [os.path.join(CSRC, src), "-o", obj]))
+        objs.append(obj)
+    logs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"]))
     os.replace(LIB + ".tmp", LIB)
     if stats or verbose:
-        print(err)
+        print("\n".join(l for l in logs if l))
     return LIB
 
 

@@ -11,14 +11,16 @@
 //
 // Work split: one workgroup of 4 waves owns 128 keys (two reference key tiles) of one (b,h);
 // wave w owns keys 32w..32w+31 and keeps their K and V rows in registers as matrix-core B
-// operands, plus fp32 dK^T/dV^T accumulators that are rounded to bf16 after every 64-row
-// query block (the reference's rounding points). Per query block the workgroup stages Q, dO
-// (row-major, swizzled) and lse/D in LDS; each wave computes S and dP for its keys (lane = key),
-// forms P and dS in registers, writes dS to LDS as [key][q], and updates dV^T/dK^T with A
-// operands read by ds_read_b64_tr_b16 from the dO/Q tiles. After a barrier the workgroup
-// computes the dQ block [64 q][D] from dS (tr reads of [key][q]) and the K block staged in LDS,
-// one bf16-rounded part per reference key tile, and adds it to dQ with fp32 atomics.
-// Query blocks entirely above a wave's keys are skipped (nothing of them is on the causal side).
+// operands, plus fp32 dK^T/dV^T accumulators rounded to bf16 after every 64-row query block
+// (the reference's rounding points). K is also staged once, transposed, for the dQ product.
+// Per 64-row query block the workgroup stages Q and dO twice -- row-major [q][d] and transposed
+// [d][q] -- plus lse and D, so that every matrix-core operand is one conflict-free 16-byte LDS
+// read at a per-lane base plus a compile-time offset. Each wave computes S and dP for its keys
+// one 32-row subtile at a time (lane = key), forms P and dS in registers, stores dS as [q][key],
+// and updates dV^T/dK^T (A operands from the transposed tiles). After a barrier each wave
+// computes its share of the dQ block [64 q][D] from dS and the transposed K, one bf16-rounded
+// part per reference key tile, and adds it to dQ with fp32 atomics. Query blocks entirely above
+// a wave's keys are skipped; the dQ product skips the same key halves.
 //
 // Matrix-core passes, as the oracle models them: S and dP sum d in passes of 8 consecutive
 // values; dK/dV sum q in passes {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}; dQ sums keys
@@ -33,30 +35,43 @@ struct BwdCfg {
   static constexpr int BN = kBwdBlockN;  // keys per workgroup
   static constexpr int BM = kTile;       // query rows per step (the reference's query tile)
   static constexpr int THREADS = 256;
-  static constexpr int CH = D / 8;
+  static constexpr int KTP = BN + 8;     // transposed K pitch [D][BN]
+  static constexpr int QP = D + 8;       // row-major Q / dO pitch [BM][D]
+  static constexpr int QTP = BM + 8;     // transposed Q / dO pitch [D][BM]
+  static constexpr int SP = BN + 8;      // dS pitch [BM][BN]
+  static constexpr int KT_ELEMS = D * KTP;
+  static constexpr int Q_ELEMS = BM * QP;
+  static constexpr int QT_ELEMS = D * QTP;
+  static constexpr int S_ELEMS = BM * SP;
   static constexpr int KC = D / 16;
   static constexpr int DT = D / 32;
-  static constexpr int K_ELEMS = BN * D;
-  static constexpr int Q_ELEMS = BM * D;
-  static constexpr int DS_ELEMS = BN * BM;
-  static constexpr int QLOADS = BM * CH / THREADS;  // 16-byte loads per thread per tensor
-  static constexpr int KLOADS = BN * CH / THREADS;
-  // dQ tiles (32 q x 32 d) per wave: (BM/32)*(D/32) tiles over 4 waves
-  static constexpr int DQ_TILES = (BM / 32) * DT / 4;
+  static constexpr int QROWS = D / 32;         // query rows per thread in the Q/dO loader
+  static constexpr int QGROUPS = BM / QROWS;   // row groups across threads
+  static constexpr int KROWS = BN * D / (8 * THREADS);  // keys per thread in the K loader (8 or 4)
+  static constexpr int KGROUPS = BN / KROWS;
+  static constexpr int DQ_TILES = (BM / 32) * DT / 4;   // 32x32 dQ tiles per wave
 };
 
+// Position of row k (0..63) inside a transposed-tile row: chunk of 16, stored in the order
+// {0-3, 8-11, 4-7, 12-15} (the q order of a 32x32 accumulator's lane halves).
+__device__ __forceinline__ int perm_pos_b(int k) {
+  return (k & ~15) + 8 * ((k >> 2) & 1) + 4 * ((k >> 3) & 1) + (k & 3);
+}
+__device__ __forceinline__ uint32_t pk_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pk_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
 template <int D>
-__global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(256, 1) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
-  using SwD = SwzTile<D>;
-  using SwS = SwzTile<C::BM>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[C::K_ELEMS + 2 * C::Q_ELEMS + C::DS_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[C::KT_ELEMS + 2 * C::Q_ELEMS + 2 * C::QT_ELEMS + C::S_ELEMS];
   __shared__ __attribute__((aligned(16))) float lse_s[C::BM];
   __shared__ __attribute__((aligned(16))) float dd_s[C::BM];
-  uint16_t* Ks = smem;
-  uint16_t* Qs = Ks + C::K_ELEMS;
+  uint16_t* Kt = smem;
+  uint16_t* Qs = Kt + C::KT_ELEMS;
   uint16_t* Gs = Qs + C::Q_ELEMS;
-  uint16_t* dSs = Gs + C::Q_ELEMS;
+  uint16_t* Qt = Gs + C::Q_ELEMS;
+  uint16_t* Gt = Qt + C::QT_ELEMS;
+  uint16_t* dSs = Gt + C::QT_ELEMS;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, l32 = lane & 31;
@@ -78,13 +93,31 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
   const bool wave_keys = kw < a.T;
   const int key = kw + l32;       // this lane's key (column of S / dP)
 
-  // ---- K block -> LDS (rows past T zero-filled); own K/V rows -> registers ----
+  // ---- K block, transposed -> LDS (keys past T zero-filled); own K/V rows -> registers ----
+  {
+    const int kg = tid % C::KGROUPS, g = tid / C::KGROUPS;  // keys KROWS*kg.., d 8g..8g+7
+    u32x4 kr[C::KROWS];
 #pragma unroll
-  for (int i = 0; i < C::KLOADS; ++i) {
-    const int idx = tid + i * C::THREADS, row = idx / C::CH, ch = idx % C::CH;
-    u32x4 v = {0, 0, 0, 0};
-    if (k0 + row < a.T) v = *(const u32x4*)(Kg + (size_t)(k0 + row) * rs + ch * 8);
-    *(u32x4*)(Ks + SwD::off(row, ch * 8)) = v;
+    for (int i = 0; i < C::KROWS; ++i) {
+      const int row = C::KROWS * kg + i;
+      kr[i] = (k0 + row < a.T) ? *(const u32x4*)(Kg + (size_t)(k0 + row) * rs + 8 * g) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int w = j >> 1;
+      uint16_t* dst = Kt + (8 * g + j) * C::KTP + C::KROWS * kg;
+      if (C::KROWS == 8) {
+        u32x4 o;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) o[p] = (j & 1) ? pk_hi(kr[2 * p][w], kr[2 * p + 1][w]) : pk_lo(kr[2 * p][w], kr[2 * p + 1][w]);
+        *(u32x4*)dst = o;
+      } else {
+        u32x2 o;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) o[p] = (j & 1) ? pk_hi(kr[2 * p][w], kr[2 * p + 1][w]) : pk_lo(kr[2 * p][w], kr[2 * p + 1][w]);
+        *(u32x2*)dst = o;
+      }
+    }
   }
   u32x4 Kr[C::KC], Vr[C::KC];
 #pragma unroll
@@ -104,15 +137,16 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
     dVa[i] = zero16();
   }
 
+  // ---- per query block loader: QROWS rows x 8 d per thread, stored row-major and transposed ----
   const int nqb = a.T / C::BM;
   const int qb0 = k0 / C::BM;
-  u32x4 qreg[C::QLOADS], greg[C::QLOADS];
+  const int qg = tid % C::QGROUPS, dg = tid / C::QGROUPS;
+  u32x4 qreg[C::QROWS], greg[C::QROWS];
   float sreg = 0.0f;
   auto gload = [&](int qb) {
 #pragma unroll
-    for (int i = 0; i < C::QLOADS; ++i) {
-      const int idx = tid + i * C::THREADS, row = idx / C::CH, ch = idx % C::CH;
-      const size_t g = (size_t)(qb * C::BM + row) * rs + ch * 8;
+    for (int i = 0; i < C::QROWS; ++i) {
+      const size_t g = (size_t)(qb * C::BM + C::QROWS * qg + i) * rs + 8 * dg;
       qreg[i] = *(const u32x4*)(Qg + g);
       greg[i] = *(const u32x4*)(Gg + g);
     }
@@ -121,15 +155,31 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
     else if (tid < 2 * C::BM)
       sreg = dd_g[qb * C::BM + tid - C::BM];
   };
+  auto tstore = [&](uint16_t* dstT, const u32x4* r) {
+    uint16_t* row0 = dstT + 8 * dg * C::QTP + perm_pos_b(C::QROWS * qg);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int w = j >> 1;
+      if (C::QROWS == 4) {
+        u32x2 o;
+        o[0] = (j & 1) ? pk_hi(r[0][w], r[1][w]) : pk_lo(r[0][w], r[1][w]);
+        o[1] = (j & 1) ? pk_hi(r[2][w], r[3][w]) : pk_lo(r[2][w], r[3][w]);
+        *(u32x2*)(row0 + j * C::QTP) = o;
+      } else {
+        *(uint32_t*)(row0 + j * C::QTP) = (j & 1) ? pk_hi(r[0][w], r[1][w]) : pk_lo(r[0][w], r[1][w]);
+      }
+    }
+  };
   auto lstore = [&]() {
 #pragma unroll
-    for (int i = 0; i < C::QLOADS; ++i) {
-      const int idx = tid + i * C::THREADS, row = idx / C::CH, ch = idx % C::CH;
-      *(u32x4*)(Qs + SwD::off(row, ch * 8)) = qreg[i];
-      *(u32x4*)(Gs + SwD::off(row, ch * 8)) = greg[i];
+    for (int i = 0; i < C::QROWS; ++i) {
+      *(u32x4*)(Qs + (C::QROWS * qg + i) * C::QP + 8 * dg) = qreg[i];
+      *(u32x4*)(Gs + (C::QROWS * qg + i) * C::QP + 8 * dg) = greg[i];
     }
+    tstore(Qt, qreg);
+    tstore(Gt, greg);
     if (tid < C::BM)
-      lse_s[tid] = sreg;
+      lse_s[tid] = sreg * kLog2e;  // the exponent is evaluated in base 2
     else if (tid < 2 * C::BM)
       dd_s[tid - C::BM] = sreg;
   };
@@ -138,41 +188,36 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
   lstore();
   __syncthreads();
 
-  const int cb = 16 * ((lane >> 4) & 1);  // column base of this lane's 16-lane group
+  const float sl = a.scale * kLog2e;
   for (int qb = qb0; qb < nqb; ++qb) {
     if (qb + 1 < nqb) gload(qb + 1);
     const int qbase = qb * C::BM;
     const bool active = wave_keys && kw <= qbase + C::BM - 1;
     if (active) {
-      // ---- S = Q.K^T and dP = dO.V^T for 64 q x this wave's 32 keys (lane = key) ----
-      f32x16 S[2], dP[2];
+      const bool diag = kw + 31 > qbase;
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs) {
-        S[qs] = zero16();
-        dP[qs] = zero16();
+        // ---- S = Q.K^T and dP = dO.V^T for 32 q x this wave's 32 keys (lane = key) ----
+        const uint16_t* qa = Qs + (32 * qs + l32) * C::QP + 8 * h;
+        const uint16_t* ga = Gs + (32 * qs + l32) * C::QP + 8 * h;
+        f32x16 S = zero16(), dP = zero16();
 #pragma unroll
         for (int c = 0; c < C::KC; ++c) {
-          const u32x4 qa = lds_read16(Qs + SwD::off(32 * qs + l32, 16 * c + 8 * h));
-          const u32x4 ga = lds_read16(Gs + SwD::off(32 * qs + l32, 16 * c + 8 * h));
-          S[qs] = mfma(qa, Kr[c], S[qs]);
-          dP[qs] = mfma(ga, Vr[c], dP[qs]);
+          S = mfma(lds_read16(qa + 16 * c), Kr[c], S);
+          dP = mfma(lds_read16(ga + 16 * c), Vr[c], dP);
         }
-      }
-      // ---- P and dS (rows q = 32qs + 8g + 4h + i) ----
-      const bool diag = kw + 31 > qbase;
-      uint32_t Pw[2][8], dSw[2][8];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
+        // ---- P and dS for rows q = 32qs + 8g + 4h + i ----
+        uint32_t Pw[8], dSw[8];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int ql = 32 * qs + 8 * g + 4 * h;
           const f32x4 lv = *(const f32x4*)(lse_s + ql);
           const f32x4 dv = *(const f32x4*)(dd_s + ql);
-          float sv[4], pv[4], dpv[4], dsv[4];
+          float sv[4], dpv[4], pv[4], dsv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            sv[i] = S[qs][4 * g + i];
-            dpv[i] = dP[qs][4 * g + i];
+            sv[i] = S[4 * g + i];
+            dpv[i] = dP[4 * g + i];
           }
           round_pair(sv[0], sv[1]);
           round_pair(sv[2], sv[3]);
@@ -180,33 +225,34 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
           round_pair(dpv[2], dpv[3]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float xs = sv[i] * a.scale;
-            float p = exp2_hw((xs - lv[i]) * kLog2e);
+            float p = exp2_hw(fmaf(sv[i], sl, -lv[i]));
             if (diag && key > qbase + ql + i) p = 0.0f;
             pv[i] = p;
-            const float t1 = p * (dpv[i] - dv[i]);
-            dsv[i] = t1 * a.scale;
+            dsv[i] = (p * (dpv[i] - dv[i])) * a.scale;
           }
-          Pw[qs][2 * g] = pack_bf16(pv[0], pv[1]);
-          Pw[qs][2 * g + 1] = pack_bf16(pv[2], pv[3]);
-          dSw[qs][2 * g] = pack_bf16(dsv[0], dsv[1]);
-          dSw[qs][2 * g + 1] = pack_bf16(dsv[2], dsv[3]);
-          *(u32x2*)(dSs + SwS::off(32 * wave + l32, ql)) = u32x2{dSw[qs][2 * g], dSw[qs][2 * g + 1]};
+          Pw[2 * g] = pack_bf16(pv[0], pv[1]);
+          Pw[2 * g + 1] = pack_bf16(pv[2], pv[3]);
+          dSw[2 * g] = pack_bf16(dsv[0], dsv[1]);
+          dSw[2 * g + 1] = pack_bf16(dsv[2], dsv[3]);
+          uint16_t* dcol = dSs + ql * C::SP + 32 * wave + l32;
+          dcol[0] = (uint16_t)dSw[2 * g];
+          dcol[C::SP] = (uint16_t)(dSw[2 * g] >> 16);
+          dcol[2 * C::SP] = (uint16_t)dSw[2 * g + 1];
+          dcol[3 * C::SP] = (uint16_t)(dSw[2 * g + 1] >> 16);
         }
-      // ---- dV^T += dO^T.P and dK^T += Q^T.dS (m = d, n = key, k = q) ----
+        // ---- dV^T += dO^T.P and dK^T += Q^T.dS over these 32 q (m = d, n = key) ----
 #pragma unroll
-      for (int cq = 0; cq < 4; ++cq) {
-        const int qs = cq >> 1, w0 = 4 * (cq & 1);
-        const u32x4 Bp = {Pw[qs][w0], Pw[qs][w0 + 1], Pw[qs][w0 + 2], Pw[qs][w0 + 3]};
-        const u32x4 Bs = {dSw[qs][w0], dSw[qs][w0 + 1], dSw[qs][w0 + 2], dSw[qs][w0 + 3]};
+        for (int half = 0; half < 2; ++half) {
+          const int cq = 2 * qs + half, w0 = 4 * half;
+          const u32x4 Bp = {Pw[w0], Pw[w0 + 1], Pw[w0 + 2], Pw[w0 + 3]};
+          const u32x4 Bs = {dSw[w0], dSw[w0 + 1], dSw[w0 + 2], dSw[w0 + 3]};
+          const uint16_t* gt = Gt + l32 * C::QTP + 16 * cq + 8 * h;
+          const uint16_t* qt = Qt + l32 * C::QTP + 16 * cq + 8 * h;
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
-          const u32x2 glo = lds_tr(tr_addr<D>(Gs, 16 * cq + 4 * h, 32 * dt + cb, lane));
-          const u32x2 ghi = lds_tr(tr_addr<D>(Gs, 16 * cq + 8 + 4 * h, 32 * dt + cb, lane));
-          dVa[dt] = mfma(u32x4{glo[0], glo[1], ghi[0], ghi[1]}, Bp, dVa[dt]);
-          const u32x2 qlo = lds_tr(tr_addr<D>(Qs, 16 * cq + 4 * h, 32 * dt + cb, lane));
-          const u32x2 qhi = lds_tr(tr_addr<D>(Qs, 16 * cq + 8 + 4 * h, 32 * dt + cb, lane));
-          dKa[dt] = mfma(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, Bs, dKa[dt]);
+          for (int dt = 0; dt < C::DT; ++dt) {
+            dVa[dt] = mfma(lds_read16(gt + 32 * dt * C::QTP), Bp, dVa[dt]);
+            dKa[dt] = mfma(lds_read16(qt + 32 * dt * C::QTP), Bs, dKa[dt]);
+          }
         }
       }
       // the reference stores dK/dV as bf16 after every query tile
@@ -217,11 +263,6 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
           round_pair(dKa[dt], r);
           round_pair(dVa[dt], r);
         }
-    } else {
-      // keys of this wave see nothing of this query block: dS rows are zero
-#pragma unroll
-      for (int g = 0; g < 8; ++g)
-        *(u32x2*)(dSs + SwS::off(32 * wave + l32, 8 * g + 4 * h)) = u32x2{0, 0};
     }
     __syncthreads();  // dS complete; Q/dO tiles no longer read
     if (qb + 1 < nqb) lstore();
@@ -231,21 +272,17 @@ __global__ void __launch_bounds__(256) bwd_kernel(BwdArgs a) {
     for (int t = 0; t < C::DQ_TILES; ++t) {
       const int tile = wave * C::DQ_TILES + t;
       const int qs = tile / C::DT, dt = tile % C::DT;
+      const uint16_t* sa = dSs + (32 * qs + l32) * C::SP + 8 * h;
+      const uint16_t* kb_ = Kt + (32 * dt + l32) * C::KTP + 8 * h;
       f32x16 sum = zero16();
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int kref = k0 / kTile + half;  // the reference key tile of these 64 keys
-        if (k0 + 64 * half >= a.T || kref > qb) continue;
+        // keys of the reference key tile 2kb+half: present, and at or below this query tile
+        if (k0 + 64 * half >= a.T || 2 * kb + half > qb) continue;
         f32x16 acc = zero16();
 #pragma unroll
-        for (int ck = 0; ck < 4; ++ck) {
-          const int kr = 64 * half + 16 * ck + 8 * h;
-          const u32x2 slo = lds_tr(tr_addr<C::BM>(dSs, kr, 32 * qs + cb, lane));
-          const u32x2 shi = lds_tr(tr_addr<C::BM>(dSs, kr + 4, 32 * qs + cb, lane));
-          const u32x2 klo = lds_tr(tr_addr<D>(Ks, kr, 32 * dt + cb, lane));
-          const u32x2 khi = lds_tr(tr_addr<D>(Ks, kr + 4, 32 * dt + cb, lane));
-          acc = mfma(u32x4{slo[0], slo[1], shi[0], shi[1]}, u32x4{klo[0], klo[1], khi[0], khi[1]}, acc);
-        }
+        for (int ck = 0; ck < 4; ++ck)
+          acc = mfma(lds_read16(sa + 64 * half + 16 * ck), lds_read16(kb_ + 64 * half + 16 * ck), acc);
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
           round_pair(acc, r);
