@@ -62,7 +62,7 @@ __host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, 
 }
 
 constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
-constexpr int kBwdBlockN = 128;  // keys owned by one backward workgroup
+constexpr int kBwdBlockN = 256;  // keys owned by one backward workgroup
 constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)
 
 }  // namespace mla
