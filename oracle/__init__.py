@@ -16,12 +16,18 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle_attn.so")
+_SRC = os.path.join(_HERE, "attn_oracle.cpp")
 
 GEMM_CHUNK16 = 0
 GEMM_SEQ = 1
 GEMM_MFMA = 2
+PASS_SEQ8 = 0
+PASS_IL4 = 1
 BWD_REFERENCE = 0
 BWD_FP32 = 1
+
+# Tensor ids of the seeded input generator.
+TID_Q, TID_K, TID_V, TID_DO = 1, 2, 3, 4
 
 
 class AttentionParams(ctypes.Structure):
@@ -44,26 +50,15 @@ def build(force: bool = False) -> str:
     return _LIB_PATH
 
 
-_lib = None
-
-
-def lib():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(_LIB_PATH):
-            build()
-        L = ctypes.CDLL(_LIB_PATH)
-        u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
-        f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
-        pp = ctypes.POINTER(AttentionParams)
-        op = ctypes.POINTER(OracleOpts)
-        L.oracle_forward.argtypes = [u16p, u16p, u16p, u16p, f32p, pp, op]
-        L.oracle_compute_d.argtypes = [u16p, u16p, f32p, pp, op]
-        L.oracle_backward.argtypes = [u16p, f32p, f32p, u16p, u16p, u16p, f32p, u16p, u16p, pp, op]
-        L.oracle_fill_normal_bf16.argtypes = [u16p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float]
-        L.oracle_fill_normal_bf16.restype = None
-        _lib = L
-    return _lib
+def build_mutant(n: int) -> str:
+    """Compiles the oracle with planted mistake `n` (ORACLE_MUTANT) into oracle/_mutants/."""
+    out_dir = os.path.join(_HERE, "_mutants")
+    os.makedirs(out_dir, exist_ok=True)
+    path = os.path.join(out_dir, f"liboracle_m{n}.so")
+    if not os.path.exists(path) or os.path.getmtime(path) < os.path.getmtime(_SRC):
+        subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", f"-DORACLE_MUTANT={n}",
+                        "-shared", "-o", path, _SRC], check=True)
+    return path
 
 
 def params(B: int, T: int, H: int, D: int) -> AttentionParams:
@@ -75,45 +70,95 @@ def opts(threads: int = 0, b_begin: int = 0, b_end: int = 0, gemm_model: int = G
     return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round)
 
 
-# Tensor ids of the seeded input generator.
-TID_Q, TID_K, TID_V, TID_DO = 1, 2, 3, 4
-
-
-def normal_bf16(shape, seed: int, tensor_id: int, scale: float = 1.0) -> np.ndarray:
-    """Seeded N(0,1)*scale bf16 bits; element i keyed by (seed, tensor_id, flat index i)."""
-    out = np.empty(int(np.prod(shape)), dtype=np.uint16)
-    lib().oracle_fill_normal_bf16(out, out.size, seed, tensor_id, scale)
-    return out.reshape(shape)
-
-
 def _check(rc: int, what: str):
     if rc != 0:
         raise ValueError(f"oracle {what} rejected the arguments (rc={rc})")
 
 
+class Oracle:
+    """One loaded build of the oracle library."""
+
+    def __init__(self, path: str):
+        L = ctypes.CDLL(path)
+        u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+        f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+        pp = ctypes.POINTER(AttentionParams)
+        op = ctypes.POINTER(OracleOpts)
+        L.oracle_forward.argtypes = [u16p, u16p, u16p, u16p, f32p, pp, op]
+        L.oracle_compute_d.argtypes = [u16p, u16p, f32p, pp, op]
+        L.oracle_backward.argtypes = [u16p, f32p, f32p, u16p, u16p, u16p, f32p, u16p, u16p, pp, op]
+        L.oracle_fill_normal_bf16.argtypes = [u16p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float]
+        L.oracle_fill_normal_bf16.restype = None
+        L.oracle_dot.argtypes = [ctypes.c_float, f32p, f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.oracle_dot.restype = ctypes.c_float
+        self.lib = L
+
+    def forward(self, q, k, v, o: OracleOpts | None = None):
+        B, T, H, D = q.shape
+        out = np.zeros_like(q)
+        lse = np.zeros((B, H, T), dtype=np.float32)
+        _check(self.lib.oracle_forward(q, k, v, out, lse, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())),
+               "forward")
+        return out, lse
+
+    def compute_d(self, dO, O, o: OracleOpts | None = None):
+        B, T, H, D = dO.shape
+        Dv = np.zeros((B, H, T), dtype=np.float32)
+        _check(self.lib.oracle_compute_d(dO, O, Dv, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())),
+               "computeD")
+        return Dv
+
+    def backward(self, dO, Dv, lse, q, k, v, o: OracleOpts | None = None):
+        B, T, H, D = q.shape
+        dQ = np.zeros((B, T, H, D), dtype=np.float32)
+        dK = np.zeros_like(q)
+        dV = np.zeros_like(q)
+        _check(self.lib.oracle_backward(dO, Dv, lse, q, k, v, dQ, dK, dV, ctypes.byref(params(B, T, H, D)),
+                                        ctypes.byref(o or opts())), "backward")
+        return dQ, dK, dV
+
+    def dot(self, acc: float, a, b, model: int = GEMM_MFMA, layout: int = PASS_SEQ8) -> float:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        return float(self.lib.oracle_dot(acc, a, b, a.size, model, layout))
+
+    def normal_bf16(self, shape, seed: int, tensor_id: int, scale: float = 1.0) -> np.ndarray:
+        out = np.empty(int(np.prod(shape)), dtype=np.uint16)
+        self.lib.oracle_fill_normal_bf16(out, out.size, seed, tensor_id, scale)
+        return out.reshape(shape)
+
+
+_DEFAULT = None
+
+
+def default() -> Oracle:
+    global _DEFAULT
+    if _DEFAULT is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _DEFAULT = Oracle(_LIB_PATH)
+    return _DEFAULT
+
+
+def lib():
+    return default().lib
+
+
+def normal_bf16(shape, seed: int, tensor_id: int, scale: float = 1.0) -> np.ndarray:
+    """Seeded N(0,1)*scale bf16 bits; element i keyed by (seed, tensor_id, flat index i)."""
+    return default().normal_bf16(shape, seed, tensor_id, scale)
+
+
 def forward(q, k, v, o: OracleOpts | None = None):
-    B, T, H, D = q.shape
-    out = np.zeros_like(q)
-    lse = np.zeros((B, H, T), dtype=np.float32)
-    _check(lib().oracle_forward(q, k, v, out, lse, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())), "forward")
-    return out, lse
+    return default().forward(q, k, v, o)
 
 
 def compute_d(dO, O, o: OracleOpts | None = None):
-    B, T, H, D = dO.shape
-    Dv = np.zeros((B, H, T), dtype=np.float32)
-    _check(lib().oracle_compute_d(dO, O, Dv, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())), "computeD")
-    return Dv
+    return default().compute_d(dO, O, o)
 
 
 def backward(dO, Dv, lse, q, k, v, o: OracleOpts | None = None):
-    B, T, H, D = q.shape
-    dQ = np.zeros((B, T, H, D), dtype=np.float32)
-    dK = np.zeros_like(q)
-    dV = np.zeros_like(q)
-    _check(lib().oracle_backward(dO, Dv, lse, q, k, v, dQ, dK, dV, ctypes.byref(params(B, T, H, D)),
-                                 ctypes.byref(o or opts())), "backward")
-    return dQ, dK, dV
+    return default().backward(dO, Dv, lse, q, k, v, o)
 
 
 def bf16_to_f32(x: np.ndarray) -> np.ndarray:

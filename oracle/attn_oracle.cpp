@@ -29,15 +29,23 @@
 // The reference's tile products run in Apple's closed matmul2d (attention.metal:93-106,240-260),
 // whose fp32 accumulation order is not published. Three models are offered for it:
 //   GEMM_MFMA    : the arithmetic of gfx950's v_mfma_f32_32x32x16_bf16, measured with in-bounds
-//                  probes: each 16-deep step is two 8-product passes; in a pass every product and
-//                  the incoming fp32 accumulator are truncated toward zero to a multiple of
-//                  2^(E-24), E = max over the pass of exp(a)+exp(b), and the exact fixed-point sum
-//                  is rounded once to fp32 (nearest even). Which k indices share a pass is the
+//                  probes: each 16-deep step is two 8-product passes; in a pass every product is
+//                  truncated toward zero and the incoming fp32 accumulator toward -infinity to a
+//                  multiple of 2^(E-24), E = max over the pass of exp(a)+exp(b), and the exact
+//                  fixed-point sum is rounded once to fp32 (nearest even). Which k indices share a pass is the
 //                  kernel's lane assignment, given per product below (PASS_SEQ8 / PASS_IL4).
 //                  Default: it makes S (hence LSE) comparable bit for bit with the GPU.
 //   GEMM_CHUNK16 : acc = RN32(acc + exact sum of 16 consecutive products) per 16 terms.
 //   GEMM_SEQ     : plain sequential fp32 accumulation over k.
 // Everything else (indices, mask, softmax recurrence, rounding points) is fixed by the source.
+//
+// ORACLE_MUTANT (compile-time, 0 = none) plants one deliberate mistake so the tests can show
+// that their checks catch it: 1 causal mask includes the diagonal, 2 scale 1/D instead of
+// 1/sqrt(D), 3 no rescale of O when the running max moves, 4 dS without the -D term,
+// 5 dV accumulated from dS instead of P. Only tests build mutants.
+#ifndef ORACLE_MUTANT
+#define ORACLE_MUTANT 0
+#endif
 #include <cstdint>
 #include <cstring>
 #include <cmath>
@@ -161,9 +169,9 @@ struct Mat {
   }
 };
 
-// One MFMA pass: acc plus the 8 products a[ix[i]]*b[ix[i]] (decoded operands). Every product
-// and acc are truncated toward zero to a multiple of 2^(E-24), E = max exp(a)+exp(b) over the
-// nonzero products, and the exact sum is rounded once to fp32.
+// One MFMA pass: acc plus the 8 products a[ix[i]]*b[ix[i]] (decoded operands). Every product is
+// truncated toward zero and acc toward -infinity to a multiple of 2^(E-24), E = max
+// exp(a)+exp(b) over the nonzero products, and the exact sum is rounded once to fp32.
 inline float mfma_pass(float acc, const int32_t* am, const int32_t* ae, const int32_t* bm, const int32_t* be,
                        const int* ix) {
   int32_t pm[8], pe[8];
@@ -194,9 +202,17 @@ inline float mfma_pass(float acc, const int32_t* am, const int32_t* ae, const in
     // |sum| < 2^29 units; with sh >= 31 it stays below a quarter ulp of acc: the result is acc
     if (sh >= 31) return acc;
     int64_t au;
-    if (sh >= 0) au = M << sh;
-    else au = (sh > -25) ? (M >> (-sh)) : 0;
-    sum += (u >> 31) ? -au : au;
+    if (sh >= 0) {
+      au = M << sh;
+      sum += (u >> 31) ? -au : au;
+    } else {
+      // the accumulator is truncated toward -infinity (products toward zero)
+      const int s = -sh;
+      if (u >> 31)
+        sum -= (s >= 40) ? 1 : (M + (int64_t)((1ll << s) - 1)) >> s;
+      else
+        sum += (s >= 40) ? 0 : (M >> s);
+    }
   }
   return round_fixed_to_f32(sum, q);
 }
@@ -305,7 +321,7 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
   gather_head(k, p, b, h, K);
   gather_head(v, p, b, h, V);
   P.resize(TILE, TILE);
-  const float scale = 1.0f / std::sqrt((float)D);  // d_sqrt, attention.metal:109
+  const float scale = (ORACLE_MUTANT == 2) ? 1.0f / (float)D : 1.0f / std::sqrt((float)D);  // d_sqrt, attention.metal:109
   std::vector<float> O((size_t)TILE * D), S((size_t)TILE * TILE), m(TILE), l(TILE);
   for (int qt = 0; qt < ntiles; ++qt) {
     std::fill(O.begin(), O.end(), 0.0f);               // :81
@@ -317,7 +333,8 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
         for (int c = 0; c < TILE; ++c) {
           const int gcol = kt * TILE + c;                                   // :117-118
           const float sv = bf(dot_model(0.0f, Q, (size_t)grow * D, K, (size_t)gcol * D, D, model, PASS_SEQ8));  // :113
-          const float masked = (gcol > grow) ? -INFINITY : 0.0f;            // :119-120
+          const bool future = (ORACLE_MUTANT == 1) ? (gcol >= grow && gcol > 0) : (gcol > grow);
+          const float masked = future ? -INFINITY : 0.0f;                   // :119-120
           S[(size_t)r * TILE + c] = bf(sv * scale + masked);                // :116,120
         }
       }
@@ -333,7 +350,8 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
           P.f[(size_t)r * TILE + c] = bf(e);
           sum += e;
         }
-        for (int d = 0; d < D; ++d) O[(size_t)r * D + d] *= a;
+        if (ORACLE_MUTANT != 3)
+          for (int d = 0; d < D; ++d) O[(size_t)r * D + d] *= a;
         m[r] = mx;
         l[r] = l[r] * a + sum;
       }
@@ -392,7 +410,7 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
           float val = std::exp(x - lv);
           if (kt == qt && c > r) val = 0.0f;
           const float Pb = bf(val);
-          const float t1 = val * (dP[(size_t)r * TILE + c] - dv);
+          const float t1 = val * (dP[(size_t)r * TILE + c] - ((ORACLE_MUTANT == 4) ? 0.0f : dv));
           const float dsv = bf(t1 * scale);
           Pt.f[(size_t)c * TILE + r] = Pb;
           dS.f[(size_t)r * TILE + c] = dsv;
@@ -414,7 +432,8 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
       for (int c = 0; c < TILE; ++c)
         for (int d = 0; d < D; ++d) {
           float kacc = dot_model(dKt[(size_t)c * D + d], dSt, (size_t)c * TILE, Qt, (size_t)d * TILE, TILE, model, PASS_IL4);
-          float vacc = dot_model(dVt[(size_t)c * D + d], Pt, (size_t)c * TILE, Gt, (size_t)d * TILE, TILE, model, PASS_IL4);
+          float vacc = dot_model(dVt[(size_t)c * D + d], (ORACLE_MUTANT == 5) ? dSt : Pt, (size_t)c * TILE, Gt,
+                                 (size_t)d * TILE, TILE, model, PASS_IL4);
           if (mode == BWD_REFERENCE) {
             kacc = bf(kacc);
             vacc = bf(vacc);

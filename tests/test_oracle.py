@@ -1,0 +1,218 @@
+"""Pins the CPU oracle (oracle/attn_oracle.cpp) without running the reference, which is Metal and
+cannot be built here. Each check is independent of the oracle's code:
+
+* fp64 attention written from the textbook formulas (itself checked by finite differences), which
+  the bf16-rounded oracle must match to bf16-level error;
+* closed forms: row 0 of a causal head equals V row 0 with LSE equal to its own score
+  (/root/reference/README.md:132 states the first); zero queries give a uniform prefix softmax
+  with LSE = log(i+1); V = identity exposes the attention matrix, whose future part is exactly 0;
+* backward identities: sum over keys of dV equals sum over queries of dO; sum over keys of dK ~ 0;
+* the matrix-core accumulation model against results recorded on MI355X;
+* planted mistakes (ORACLE_MUTANT builds) that these checks must reject.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+f = O.bf16_to_f32
+
+
+# ---------------------------------------------------------------- fp64 reference (per head)
+def attn64(q, k, v, g):
+    """Causal softmax attention and its gradients in fp64. q,k,v,g: [T, D]."""
+    T, D = q.shape
+    s = (q @ k.T) / np.sqrt(D)
+    s[np.triu(np.ones((T, T), bool), 1)] = -np.inf
+    m = s.max(1, keepdims=True)
+    p = np.exp(s - m)
+    l_ = p.sum(1, keepdims=True)
+    P = p / l_
+    o = P @ v
+    lse = (m + np.log(l_))[:, 0]
+    dP = g @ v.T
+    dd = (g * o).sum(1, keepdims=True)
+    dS = P * (dP - dd) / np.sqrt(D)
+    return o, lse, dS @ k, dS.T @ q, P.T @ g
+
+
+def heads(x, b, h):
+    return f(x[b, :, h, :]).astype(np.float64)
+
+
+def test_fp64_reference_gradients_by_finite_differences():
+    rng = np.random.default_rng(0)
+    T, D = 6, 4
+    q, k, v, g = (rng.standard_normal((T, D)) for _ in range(4))
+    _, _, dq, dk, dv = attn64(q, k, v, g)
+    eps = 1e-6
+    for which, grad in ((0, dq), (1, dk), (2, dv)):
+        num = np.zeros_like(grad)
+        for i in range(T):
+            for j in range(D):
+                args_p = [q.copy(), k.copy(), v.copy()]
+                args_m = [q.copy(), k.copy(), v.copy()]
+                args_p[which][i, j] += eps
+                args_m[which][i, j] -= eps
+                lp = (attn64(*args_p, g)[0] * g).sum()
+                lm = (attn64(*args_m, g)[0] * g).sum()
+                num[i, j] = (lp - lm) / (2 * eps)
+        assert np.abs(num - grad).max() < 1e-6
+
+
+# ---------------------------------------------------------------- checks shared with mutants
+def inputs(B, T, H, D, seed, s=1.0):
+    return (O.normal_bf16((B, T, H, D), seed, O.TID_Q, s), O.normal_bf16((B, T, H, D), seed, O.TID_K, s),
+            O.normal_bf16((B, T, H, D), seed, O.TID_V), O.normal_bf16((B, T, H, D), seed, O.TID_DO))
+
+
+def forward_error_vs_fp64(orc, B=1, T=128, H=2, D=64, seed=3, s=1.0):
+    q, k, v, g = inputs(B, T, H, D, seed, s)
+    out, lse = orc.forward(q, k, v)
+    eo = el = 0.0
+    for b in range(B):
+        for h in range(H):
+            o64, l64, *_ = attn64(heads(q, b, h), heads(k, b, h), heads(v, b, h), heads(g, b, h))
+            eo = max(eo, np.abs(heads(out, b, h) - o64).max())
+            el = max(el, np.abs(lse[b, h] - l64).max())
+    return eo, el
+
+
+def backward_error_vs_fp64(orc, B=1, T=128, H=2, D=64, seed=4, s=1.0):
+    q, k, v, g = inputs(B, T, H, D, seed, s)
+    out, lse = orc.forward(q, k, v)
+    Dv = orc.compute_d(g, out)
+    dQ, dK, dV = orc.backward(g, Dv, lse, q, k, v)
+    errs = [0.0, 0.0, 0.0]
+    for b in range(B):
+        for h in range(H):
+            _, _, dq, dk, dv = attn64(heads(q, b, h), heads(k, b, h), heads(v, b, h), heads(g, b, h))
+            for i, (x, r) in enumerate(((dQ[b, :, h].astype(np.float64), dq), (heads(dK, b, h), dk), (heads(dV, b, h), dv))):
+                errs[i] = max(errs[i], np.abs(x - r).max() / np.abs(r).max())
+    return errs
+
+
+def row0_and_uniform(orc, D=64):
+    T, H = 128, 2
+    q, k, v, g = inputs(1, T, H, D, 5)
+    out, lse = orc.forward(q, k, v)
+    ok_row0 = np.array_equal(out[0, 0], v[0, 0])
+    zq = np.zeros_like(q)
+    out0, lse0 = orc.forward(zq, k, v)
+    ref = np.log(np.arange(1, T + 1, dtype=np.float32))  # l = i+1 exactly, m = 0: LSE = log(i+1) to 1 ulp
+    ok_lse = bool((np.abs(lse0[0] - ref) <= np.spacing(ref)).all())
+    mean = np.cumsum(f(v[0]).astype(np.float64), axis=0) / np.arange(1, T + 1)[:, None, None]
+    ok_mean = np.abs(f(out0[0]) - mean).max() < 2e-2
+    return ok_row0, ok_lse, ok_mean
+
+
+def identity_future_zero(orc, D=64):
+    T = D
+    q, k, _, _ = inputs(1, T, 1, D, 6)
+    v = np.zeros((1, T, 1, D), np.uint16)
+    v[0, np.arange(T), 0, np.arange(T)] = 0x3F80  # bf16 1.0: V = I
+    out, _ = orc.forward(q, k, v)
+    A = f(out[0, :, 0, :])
+    return bool((A[np.triu_indices(T, 1)] == 0).all()) and np.abs(A.sum(1) - 1).max() < 2e-2
+
+
+FWD_TOL_O, FWD_TOL_LSE, BWD_TOL = 2e-2, 3e-2, 3e-2
+
+
+# ---------------------------------------------------------------- the oracle passes
+@pytest.mark.parametrize("D,s", [(64, 1.0), (128, 1.0), (64, 1.5)])
+def test_forward_matches_fp64(D, s):
+    eo, el = forward_error_vs_fp64(O.default(), D=D, s=s)
+    assert eo < FWD_TOL_O and el < FWD_TOL_LSE, (eo, el)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_backward_matches_fp64(D):
+    errs = backward_error_vs_fp64(O.default(), D=D)
+    assert max(errs) < BWD_TOL, errs
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_closed_forms(D):
+    assert row0_and_uniform(O.default(), D) == (True, True, True)
+    assert identity_future_zero(O.default(), D)
+
+
+def test_backward_identities():
+    B, T, H, D = 1, 192, 2, 64
+    q, k, v, g = inputs(B, T, H, D, 7)
+    out, lse = O.forward(q, k, v)
+    Dv = O.compute_d(g, out)
+    dQ, dK, dV = O.backward(g, Dv, lse, q, k, v)
+    # rows of P sum to 1: sum_keys dV = sum_queries dO (bf16 accumulation tolerance)
+    sdv, sdo = f(dV).sum(1), f(g).sum(1)
+    assert np.abs(sdv - sdo).max() / np.abs(sdo).max() < 2e-2
+    # rows of dS sum to ~0 (D = rowsum(dO*O)): sum_keys dK ~ 0 relative to |dK|
+    assert np.abs(f(dK).sum(1)).max() < 0.1 * np.abs(f(dK)).sum(1).max()
+    # row 0 sees only key 0: P = [1], dS = dP - D ~ 0
+    assert np.abs(dQ[:, 0]).max() < 0.05 * np.abs(dQ).max()
+
+
+def test_compute_d_against_fp64_and_rounding():
+    q, k, v, g = inputs(2, 64, 3, 128, 8)
+    out, _ = O.forward(q, k, v)
+    Dv = O.compute_d(g, out)
+    exact = (f(g).astype(np.float64) * f(out)).sum(-1).transpose(0, 2, 1)
+    assert np.abs(Dv - exact).max() <= 4e-3 * np.abs(exact).max() + 1e-6
+    assert np.array_equal(f(O.f32_to_bf16(Dv)), Dv)  # the reference stores D as bf16
+
+
+def test_batch_slice_is_independent():
+    q, k, v, g = inputs(3, 64, 2, 64, 9)
+    a, la = O.forward(q, k, v)
+    b, lb = O.forward(q[1:2].copy(), k[1:2].copy(), v[1:2].copy())
+    assert np.array_equal(a[1:2], b) and np.array_equal(la[1:2], lb)
+    # keyed by flat index: batch b of a B=3 draw equals batch b of a B=1 draw
+    assert np.array_equal(O.normal_bf16((3, 64, 2, 64), 9, O.TID_Q)[:1], O.normal_bf16((1, 64, 2, 64), 9, O.TID_Q))
+
+
+def test_mfma_model_matches_recorded_hardware():
+    cases = json.load(open(os.path.join(HERE, "golden", "mfma_rounding_cases.json")))["cases"]
+    assert len(cases) >= 70
+    orc = O.default()
+    for c in cases:
+        a = np.zeros(16, np.float32)
+        b = np.zeros(16, np.float32)
+        for kk, x, y in c["terms"]:
+            a[kk] = float.fromhex(x)
+            b[kk] = float.fromhex(y)
+        got = orc.dot(float.fromhex(c["acc"]), a, b, O.GEMM_MFMA, O.PASS_SEQ8)
+        assert np.float32(got) == np.float32(float.fromhex(c["gpu"])), c["name"]
+    # and a plain fp32 model would not reproduce them
+    mism = 0
+    for c in cases:
+        a = np.zeros(16, np.float32)
+        b = np.zeros(16, np.float32)
+        for kk, x, y in c["terms"]:
+            a[kk], b[kk] = float.fromhex(x), float.fromhex(y)
+        mism += orc.dot(float.fromhex(c["acc"]), a, b, O.GEMM_SEQ) != float.fromhex(c["gpu"])
+    assert mism > 10
+
+
+def test_rejects_invalid_shapes():
+    q, k, v, _ = inputs(1, 64, 1, 64, 1)
+    with pytest.raises(ValueError):
+        O.forward(q[:, :60].copy(), k[:, :60].copy(), v[:, :60].copy())
+    q2 = np.zeros((1, 64, 1, 96), np.uint16)
+    with pytest.raises(ValueError):
+        O.forward(q2, q2, q2)
+
+
+# ---------------------------------------------------------------- planted mistakes are caught
+@pytest.mark.parametrize("mutant", [1, 2, 3, 4, 5])
+def test_planted_mistakes_are_caught(mutant):
+    orc = O.Oracle(O.build_mutant(mutant))
+    eo, el = forward_error_vs_fp64(orc)
+    fwd_bad = eo >= FWD_TOL_O or el >= FWD_TOL_LSE
+    closed_bad = row0_and_uniform(orc) != (True, True, True) or not identity_future_zero(orc)
+    bwd_bad = max(backward_error_vs_fp64(orc)) >= BWD_TOL
+    assert fwd_bad or closed_bad or bwd_bad

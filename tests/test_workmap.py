@@ -1,0 +1,28 @@
+"""Workgroup -> (head pair, block) decode of both kernels (host function shared with the device
+code): every block of every (batch, head) pair is owned by exactly one workgroup, so dK/dV rows
+(backward) and O rows (forward) have a single writer; blocks of one pair share an XCD when the
+pair count allows; the largest causal blocks are dispatched first."""
+import numpy as np
+import pytest
+
+import metalllm_amd as M
+
+
+@pytest.mark.parametrize("B,T,H,D", [(16, 256, 6, 64), (128, 256, 6, 64), (32, 1024, 12, 64), (16, 4096, 16, 128),
+                                     (1, 192, 3, 128), (3, 320, 1, 64), (1, 64, 1, 64)])
+@pytest.mark.parametrize("kind,blk,last_first", [(0, 128, True), (1, 256, False)])
+def test_partition(B, T, H, D, kind, blk, last_first):
+    wm = M.work_map(kind, B, T, H, D)
+    npairs, nblk = B * H, -(-T // blk)
+    assert wm.shape == (npairs * nblk, 2)
+    seen = set(map(tuple, wm.tolist()))
+    assert seen == {(p, b) for p in range(npairs) for b in range(nblk)}
+    # causal work of a block: forward query block qb sees qb+1 key tiles, backward key block kb
+    # sees T/64 - 4kb query tiles; within a pair the dispatch order is non-increasing in work
+    work = (wm[:, 1] + 1) if kind == 0 else (T // 64 - 4 * wm[:, 1])
+    for p in range(npairs):
+        w = work[wm[:, 0] == p]
+        assert (np.diff(w) <= 0).all()
+    if npairs % 8 == 0:  # workgroup i runs on XCD i % 8: all blocks of a pair share one XCD
+        for p in range(npairs):
+            assert len(set((np.nonzero(wm[:, 0] == p)[0] % 8).tolist())) == 1
