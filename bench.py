@@ -85,6 +85,9 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run one device copy of 256 MiB (read) -> 256 MiB (write), "
+                         "the known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -139,6 +142,13 @@ def main():
         step(events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     # per-kernel times from the events (the dQ zeroing is in the step, outside the kernel intervals)
     fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
