@@ -9,7 +9,7 @@
 //
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives column j of a 4 x 16 block
 // of bf16 (4 rows), where source lane s of the group supplies the address of row s/4, columns
-// 4(s%4)..4(s%4)+3. tr_addr() below computes that per-lane address.
+// 4(s%4)..4(s%4)+3.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -82,29 +82,5 @@ __device__ __forceinline__ u32x2 lds_tr(const uint16_t* p) {
 }
 
 __device__ __forceinline__ u32x4 lds_read16(const uint16_t* p) { return *(const u32x4*)p; }
-
-// Row-major bf16 tile in LDS with 16-byte chunks XOR-swizzled by row, so that both a 16-row
-// column of 16-byte reads and a 4-row ds_read_b64_tr_b16 block spread over distinct banks.
-// ROW = elements per row (= head dim D); rows of 2*ROW bytes, RPC rows per 256-byte bank cycle.
-template <int ROW>
-struct SwzTile {
-  static constexpr int CH = ROW / 8;          // 16-byte chunks per row
-  static constexpr int RPC = 256 / (2 * ROW);  // rows per 256-byte bank cycle (1 or 2)
-  __device__ static __forceinline__ int key(int r) {
-    const int j = r / RPC;
-    return (2 * j + j / (CH / 2)) & (CH - 1);
-  }
-  // element offset of (r, c); c % 4 == 0 keeps an 8-byte piece inside one chunk
-  __device__ static __forceinline__ int off(int r, int c) {
-    return r * ROW + (((c >> 3) ^ key(r)) << 3) + (c & 7);
-  }
-};
-
-// Per-lane address for a transposed 4x16 read of tile rows [r0, r0+4), columns [c0, c0+16).
-template <int ROW>
-__device__ __forceinline__ const uint16_t* tr_addr(const uint16_t* tile, int r0, int c0, int lane) {
-  const int s = lane & 15;
-  return tile + SwzTile<ROW>::off(r0 + (s >> 2), c0 + 4 * (s & 3));
-}
 
 }  // namespace mla
