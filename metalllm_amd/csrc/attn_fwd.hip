@@ -8,20 +8,26 @@
 //   P = bf16(e), l' = l*a + sum e (unrounded), O = O*a + P.V   (:125-153)
 //   out = bf16(O * (1/l)), lse = m + log(l)                    (:156-161)
 //
-// Work split: one workgroup of 4 waves owns 128 query rows of one (b,h); each wave owns 32
-// rows and holds its Q rows as matrix-core B operands in registers. Key tiles of 64 rows are
-// double-buffered through LDS: K row-major ([key][d], pitch D+8) and V transposed ([d][key],
-// pitch 72), so every matrix-core operand read is one conflict-free 16-byte ds_read at a
-// per-lane base plus a compile-time offset. The next tile's global loads are issued before the
-// current tile's math; key tiles entirely above a wave's diagonal are skipped and only
-// diagonal tiles apply the mask. The O rescale is skipped when no row's running max moved
-// (the factor is then exactly 1).
+// Work split: a workgroup of 4 waves owns 128 query rows of one (b,h); each wave owns 32 rows
+// and holds its Q rows as matrix-core B operands in registers. Two workgroups share a CU.
 //
 // Orientation: the wave computes S^T (keys x queries) so that lane = query column. Row
 // statistics are in-lane (16 values per 32-key subtile) plus one exchange between the two lane
-// halves; the S^T accumulator is directly the B operand (P^T) of O^T += V^T.P^T. Lane half h of
-// a 32-key subtile holds keys {8g + 4h + i}; the transposed V tile stores each 16-key chunk in
-// the order {0-3, 8-11, 4-7, 12-15} so that those 8 keys are one contiguous 16-byte read.
+// halves; the S^T accumulator, packed to bf16, is directly the B operand (P^T) of
+// O^T += V^T.P^T. Lane half h of a 32-key subtile holds keys {8g + 4h + i}; the V^T operand is
+// read with ds_read_b64_tr_b16 from the row-major V tile, four keys per read, in that order.
+//
+// Software pipeline (per wave): step j computes the softmax of tile j on the vector ALU while
+// the matrix cores compute S of tile j+1 and O += P.V of tile j-1; the instructions of the two
+// are interleaved by the scheduler. K and V tiles are copied global -> LDS by the hardware
+// (global_load_lds_dwordx4, no registers) two stages deep: step j loads K(j+2) and V(j) into
+// the stage that steps j-1 finished reading, and reads K(j+1) and V(j-1) from the other one.
+//
+// Running max: m is the reference point of the exponentials. It moves to the tile max only when
+// that exceeds m by more than 8 in log2 units (e <= 256), so the O rescale runs on a few tiles
+// per row instead of on most; l and O keep the same reference point, so out = O/l and
+// lse = m + log(l) are unchanged up to rounding. Skipping the rescale when no max moved at all is
+// the special case of threshold 0.
 //
 // Matrix-core passes, as the oracle models them: S sums d in passes of 8 consecutive values;
 // P.V sums keys in passes {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}.
@@ -32,38 +38,97 @@ namespace mla {
 
 template <int D>
 struct FwdCfg {
-  static constexpr int BM = kFwdBlockM;  // query rows per workgroup
-  static constexpr int BN = kTile;       // keys per tile
+  static constexpr int BM = kFwdBlockM;  // query rows per workgroup (128)
+  static constexpr int BN = kTile;       // keys per tile (64)
   static constexpr int THREADS = 256;
-  static constexpr int KP = D + 8;       // K tile pitch (elements): 16-row column reads hit distinct banks
-  static constexpr int VP = BN + 8;      // transposed V tile pitch
-  static constexpr int K_ELEMS = BN * KP;
-  static constexpr int V_ELEMS = D * VP;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;
-  static constexpr int CH = D / 8;                 // 16-byte chunks per row
-  static constexpr int KLOADS = BN * CH / THREADS;  // 16-byte K loads per thread per tile
-  static constexpr int VKEYS = D / 32;             // keys per thread in the V transpose (4 or 2)
-  static constexpr int VGROUPS = BN / VKEYS;       // key groups across threads (16 or 32)
-  static constexpr int KC = D / 16;                // 16-deep matrix-core steps over d
-  static constexpr int DT = D / 32;                // 32-wide d tiles of the output
+  static constexpr int KP = D + 8;                          // K row pitch (elements): b128 reads conflict-free
+  static constexpr int VP = (D == 128) ? D + 24 : D + 8;    // V row pitch: tr reads conflict-free
+  static constexpr int KSLOTS = KP / 8;                     // 16-byte slots per K row (17 / 9)
+  static constexpr int VSLOTS = VP / 8;                     // (19 / 9)
+  static constexpr int KBYTES = BN * KP * 2;                // = KSLOTS KB: one 1 KB load instruction per KB
+  static constexpr int VBYTES = BN * VP * 2;
+  static constexpr int STAGE = KBYTES + VBYTES;
+  static constexpr int KPW = (KSLOTS + 3) / 4;              // K load instructions per wave (max)
+  static constexpr int VPW = (VSLOTS + 3) / 4;
+  static constexpr int KC = D / 16;                         // 16-deep matrix-core steps over d
+  static constexpr int DT = D / 32;                         // 32-wide d tiles of the output
 };
 
-// Position of key k (0..63) inside a transposed-tile row: chunk of 16 keys, stored in the
-// order {0-3, 8-11, 4-7, 12-15}.
-__device__ __forceinline__ int perm_pos(int k) {
-  return (k & ~15) + 8 * ((k >> 2) & 1) + 4 * ((k >> 3) & 1) + (k & 3);
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Copies 64 lanes x 16 bytes from per-lane global addresses into 1 KB of LDS at `dst` (lane i
+// writes dst + 16 i).
+__device__ __forceinline__ void g2lds(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
 
-// {lo16(a), lo16(b)} and {hi16(a), hi16(b)}
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+template <int D>
+struct FwdState {
+  f32x16 O[D / 32];
+  float m_use, l_run, alpha;
+  bool rescale;
+};
+
+// Softmax of one 64-key tile held as two S^T subtiles (lane = query): rounding points, mask,
+// running max with threshold, exponentials, row sum and packed P.
+template <int D, bool MASK>
+__device__ __forceinline__ void softmax_tile(const f32x16& S0, const f32x16& S1, FwdState<D>& st, uint32_t (&P)[16],
+                                             float scale, float c1, int key0, int q, int h) {
+  float x[32];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    x[r] = S0[r];
+    x[16 + r] = S1[r];
+  }
+#pragma unroll
+  for (int i = 0; i < 32; i += 2) {
+    round_pair(x[i], x[i + 1]);
+    if (D != 64) {
+      x[i] *= scale;
+      x[i + 1] *= scale;
+      round_pair(x[i], x[i + 1]);
+    }
+  }
+  if (MASK) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int r = i & 15;
+      const int key = key0 + 32 * (i >> 4) + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (key > q) x[i] = -INFINITY;
+    }
+  }
+  float mt = fmaxf(x[0], x[1]);
+#pragma unroll
+  for (int i = 2; i < 32; i += 2) mt = fmaxf(mt, fmaxf(x[i], x[i + 1]));
+  mt = max_halves(mt);
+  // threshold 8 in log2 units; true on the first tile (m_use = -inf). Branch-free, so that the
+  // scheduler can interleave the whole tile with the matrix-core work of the pipeline step.
+  const bool need = (mt - st.m_use) * c1 > 8.0f;
+  st.rescale = __any(need);
+  const float m_new = need ? mt : st.m_use;
+  st.alpha = exp2_hw((st.m_use - m_new) * c1);  // exactly 1 where m stays, 0 on the first tile
+  st.l_run *= st.alpha;
+  st.m_use = m_new;
+  const float mb = st.m_use * c1;
+  float ls = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i += 2) {
+    const float e0 = exp2_hw(fmaf(x[i], c1, -mb));
+    const float e1 = exp2_hw(fmaf(x[i + 1], c1, -mb));
+    ls += e0;
+    ls += e1;
+    P[i >> 1] = pack_bf16(e0, e1);
+  }
+  st.l_run += ls;
+}
 
 template <int D>
 __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   using C = FwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int nqb = (a.T + C::BM - 1) / C::BM;
   int pair, qb;
@@ -72,153 +137,167 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   const int rs = a.H * D;  // elements between consecutive tokens
   const size_t base = ((size_t)b * a.T * a.H + hd) * D;
   const uint16_t* Qg = a.q + base;
-  const uint16_t* Kg = a.k + base;
-  const uint16_t* Vg = a.v + base;
+  const char* Kg = (const char*)(a.k + base);
+  const char* Vg = (const char*)(a.v + base);
+  const size_t tile_bytes = (size_t)C::BN * rs * 2;
 
   const int q0 = qb * C::BM;
   const int qw = q0 + 32 * wave;  // this wave's first query row
   const bool wave_active = qw < a.T;
-  const int q_end = min(q0 + C::BM, a.T);
-  const int last_kt = (q_end - 1) / C::BN;
-  const int q = qw + l32;  // this lane's query row
+  const int n_tiles = (min(q0 + C::BM, a.T) - 1) / C::BN + 1;  // key tiles the workgroup visits
+  const int my_tiles = wave_active ? qw / C::BN + 1 : 0;       // tiles of this wave; the last is diagonal
+  const int q = qw + l32;                                       // this lane's query row
 
   // Q^T as B operands: lane holds Q[q][16c + 8h .. +7].
   u32x4 Qr[C::KC];
 #pragma unroll
-  for (int c = 0; c < C::KC; ++c) {
-    if (wave_active)
-      Qr[c] = *(const u32x4*)(Qg + (size_t)q * rs + 16 * c + 8 * h);
-    else
-      Qr[c] = u32x4{0, 0, 0, 0};
-  }
+  for (int c = 0; c < C::KC; ++c)
+    Qr[c] = wave_active ? *(const u32x4*)(Qg + (size_t)q * rs + 16 * c + 8 * h) : u32x4{0, 0, 0, 0};
 
-  f32x16 O[C::DT];
+  // Loader: 1 KB instruction i of a tile covers 16-byte slots 64i..64i+63 of the padded tile;
+  // slot s is (row s / SLOTS, chunk s % SLOTS); pad chunks re-read the row's last chunk.
+  uint32_t koff[C::KPW], voff[C::VPW];
 #pragma unroll
-  for (int i = 0; i < C::DT; ++i) O[i] = zero16();
-  float m_run = -INFINITY, l_run = 0.0f;
+  for (int j = 0; j < C::KPW; ++j) {
+    const int s = 64 * (wave + 4 * j) + lane, row = s / C::KSLOTS, c = min(s % C::KSLOTS, D / 8 - 1);
+    koff[j] = (uint32_t)(row * rs * 2 + c * 16);
+  }
+#pragma unroll
+  for (int j = 0; j < C::VPW; ++j) {
+    const int s = 64 * (wave + 4 * j) + lane, row = s / C::VSLOTS, c = min(s % C::VSLOTS, D / 8 - 1);
+    voff[j] = (uint32_t)(row * rs * 2 + c * 16);
+  }
+  auto load_k = [&](int kt, int stage) {
+    const char* src = Kg + (size_t)kt * tile_bytes;
+    unsigned char* dst = smem + stage * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::KPW; ++j)
+      if (wave + 4 * j < C::KSLOTS) g2lds(src + koff[j], dst + 1024 * (wave + 4 * j));
+  };
+  auto load_v = [&](int kt, int stage) {
+    const char* src = Vg + (size_t)kt * tile_bytes;
+    unsigned char* dst = smem + stage * C::STAGE + C::KBYTES;
+#pragma unroll
+    for (int j = 0; j < C::VPW; ++j)
+      if (wave + 4 * j < C::VSLOTS) g2lds(src + voff[j], dst + 1024 * (wave + 4 * j));
+  };
+
+  // Per-lane LDS operand bases (element offsets inside a stage).
+  // K rows: A operand of S^T, lane = key row, 8 d at 16c + 8h.
+  const int k_rd = l32 * C::KP + 8 * h;
+  // V^T via tr reads: group g = lane/16 covers d = 16(g%2) .. +15 of a 32-d tile; source lane
+  // s = lane%16 points at key row 4h + s/4 (+8 for the second read), d offset 4(s%4).
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int v_rd = (4 * h + (s16 >> 2)) * C::VP + 16 * (g16 & 1) + 4 * (s16 & 3);
+
+  auto s_tile = [&](int stage, f32x16& S0, f32x16& S1) {
+    const uint16_t* kb = (const uint16_t*)(smem + stage * C::STAGE) + k_rd;
+    S0 = zero16();
+    S1 = zero16();
+#pragma unroll
+    for (int c = 0; c < C::KC; ++c) {
+      S0 = mfma(lds_read16(kb + 16 * c), Qr[c], S0);
+      S1 = mfma(lds_read16(kb + 32 * C::KP + 16 * c), Qr[c], S1);
+    }
+  };
+  auto pv_tile = [&](int stage, const uint32_t (&P)[16], FwdState<D>& st) {
+    const uint16_t* vb = (const uint16_t*)(smem + stage * C::STAGE + C::KBYTES) + v_rd;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 Bp = {P[4 * c], P[4 * c + 1], P[4 * c + 2], P[4 * c + 3]};
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) {
+        const u32x2 lo = lds_tr(vb + 16 * c * C::VP + 32 * dt);
+        const u32x2 hi = lds_tr(vb + (16 * c + 8) * C::VP + 32 * dt);
+        st.O[dt] = mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, Bp, st.O[dt]);
+      }
+    }
+  };
+  auto apply_rescale = [&](FwdState<D>& st) {
+    if (st.rescale) {
+      asm volatile("" ::: "memory");  // keeps the rare rescale behind its branch
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st.O[dt][r] *= st.alpha;
+    }
+  };
+
+  FwdState<D> st;
+#pragma unroll
+  for (int i = 0; i < C::DT; ++i) st.O[i] = zero16();
+  st.m_use = -INFINITY;
+  st.l_run = 0.0f;
+  st.alpha = 1.0f;
+  st.rescale = false;
   // Scores are carried in units u: s = x*su. For D=64, x = bf16(S) and su = 0.125 (exact);
   // for D=128, x = bf16(bf16(S)*scale) and su = 1.
   const float su = (D == 64) ? 0.125f : 1.0f;
   const float c1 = su * kLog2e;
 
-  // ---- tile loaders: K rows as 16-byte chunks; V as VKEYS keys x 8 d per thread ----
-  const int vg = tid / C::VGROUPS;           // d group: d = 8vg .. 8vg+7
-  const int vk = (tid % C::VGROUPS) * C::VKEYS;  // first key of this thread's group
-  u32x4 kreg[C::KLOADS], vreg[C::VKEYS];
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < C::KLOADS; ++i) {
-      const int idx = tid + i * C::THREADS, row = idx / C::CH, ch = idx % C::CH;
-      kreg[i] = *(const u32x4*)(Kg + (size_t)(kt * C::BN + row) * rs + ch * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < C::VKEYS; ++i) vreg[i] = *(const u32x4*)(Vg + (size_t)(kt * C::BN + vk + i) * rs + 8 * vg);
-  };
-  auto lstore = [&](int stage) {
-    uint16_t* Ks = smem + stage * C::STAGE;
-    uint16_t* Vt = Ks + C::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < C::KLOADS; ++i) {
-      const int idx = tid + i * C::THREADS, row = idx / C::CH, ch = idx % C::CH;
-      *(u32x4*)(Ks + row * C::KP + ch * 8) = kreg[i];
-    }
-    uint16_t* vrow = Vt + 8 * vg * C::VP + perm_pos(vk);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {  // d = 8vg + j
-      const int w = j >> 1;
-      if (C::VKEYS == 4) {
-        u32x2 o;
-        o[0] = (j & 1) ? pack_hi(vreg[0][w], vreg[1][w]) : pack_lo(vreg[0][w], vreg[1][w]);
-        o[1] = (j & 1) ? pack_hi(vreg[2][w], vreg[3][w]) : pack_lo(vreg[2][w], vreg[3][w]);
-        *(u32x2*)(vrow + j * C::VP) = o;
-      } else {
-        *(uint32_t*)(vrow + j * C::VP) = (j & 1) ? pack_hi(vreg[0][w], vreg[1][w]) : pack_lo(vreg[0][w], vreg[1][w]);
-      }
-    }
-  };
+  f32x16 Sc0 = zero16(), Sc1 = zero16(), Sn0 = zero16(), Sn1 = zero16();  // S^T: current tile, next tile
+  uint32_t Pc[16], Pp[16];     // P of the current tile, and of the previous one
 
-  gload(0);
-  lstore(0);
+  // ---- prologue: K(0) -> stage 0, K(1) -> stage 1; S(0) ----
+  load_k(0, 0);
+  if (n_tiles > 1) load_k(1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (my_tiles > 0) s_tile(0, Sc0, Sc1);
   __syncthreads();
 
-  for (int kt = 0; kt <= last_kt; ++kt) {
-    if (kt < last_kt) gload(kt + 1);
-    const uint16_t* Ks = smem + (kt & 1) * C::STAGE;
-    const uint16_t* Vt = Ks + C::K_ELEMS;
-    if (wave_active && kt * C::BN <= qw + 31) {
-      // ---- S^T = K.Q^T for 64 keys (two 32-key subtiles) x 32 queries ----
-      const uint16_t* kb = Ks + l32 * C::KP + 8 * h;
-      f32x16 S0 = zero16(), S1 = zero16();
-#pragma unroll
-      for (int c = 0; c < C::KC; ++c) {
-        S0 = mfma(lds_read16(kb + 16 * c), Qr[c], S0);
-        S1 = mfma(lds_read16(kb + 32 * C::KP + 16 * c), Qr[c], S1);
-      }
-      // ---- rounding points, mask, online softmax (lane = query q) ----
-      float x[32];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        x[r] = S0[r];
-        x[16 + r] = S1[r];
-      }
-#pragma unroll
-      for (int i = 0; i < 32; i += 2) {
-        round_pair(x[i], x[i + 1]);
-        if (D != 64) {
-          x[i] *= a.scale;
-          x[i + 1] *= a.scale;
-          round_pair(x[i], x[i + 1]);
-        }
-      }
-      if (kt * C::BN + C::BN - 1 > qw) {  // diagonal tile for this wave
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int r = i & 15;
-          const int key = kt * C::BN + 32 * (i >> 4) + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key > q) x[i] = -INFINITY;
-        }
-      }
-      float mt = x[0];
-#pragma unroll
-      for (int i = 1; i < 32; ++i) mt = fmaxf(mt, x[i]);
-      mt = max_halves(mt);
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = exp2_hw((m_run - m_new) * c1);
-      const float mb = m_new * c1;
-      uint32_t P[16];
-      float ls = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 32; i += 2) {
-        const float e0 = exp2_hw(fmaf(x[i], c1, -mb));
-        const float e1 = exp2_hw(fmaf(x[i + 1], c1, -mb));
-        ls += e0;
-        ls += e1;
-        P[i >> 1] = pack_bf16(e0, e1);
-      }
-      l_run = l_run * alpha + ls;
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) O[dt][r] *= alpha;
-      }
-      m_run = m_new;
-      // ---- O^T += V^T . P^T ----
-      const uint16_t* vb = Vt + l32 * C::VP + 8 * h;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 Bp = {P[4 * c], P[4 * c + 1], P[4 * c + 2], P[4 * c + 3]};
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) O[dt] = mfma(lds_read16(vb + 32 * dt * C::VP + 16 * c), Bp, O[dt]);
-      }
+  // One pipeline step: loads K(kt+2), V(kt) -> stage kt&1; reads K(kt+1), V(kt-1) from the other.
+  auto step = [&](int kt, bool do_s, bool do_pv, bool do_sm, bool diag) {
+    if (kt + 2 < n_tiles) load_k(kt + 2, kt & 1);
+    load_v(kt, kt & 1);
+    const int rd = (kt + 1) & 1;
+    if (do_s) s_tile(rd, Sn0, Sn1);
+    if (do_pv) pv_tile(rd, Pp, st);
+    if (do_sm) {
+      if (diag)
+        softmax_tile<D, true>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
+      else
+        softmax_tile<D, false>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
+      apply_rescale(st);
     }
-    if (kt < last_kt) lstore((kt + 1) & 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Pp[i] = Pc[i];
+    Sc0 = Sn0;
+    Sc1 = Sn1;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+
+  // Tiles 0 .. full_end-1 are below every wave's diagonal (no mask), and every wave is active.
+  const int full_end = q0 / C::BN;
+  int kt = 0;
+  if (full_end >= 2) {
+    step(0, true, false, true, false);
+    for (kt = 1; kt + 1 < full_end; ++kt) {
+      // steady state: S(kt+1) full, P.V(kt-1), softmax(kt) full; kt+2 <= full_end < n_tiles
+      load_k(kt + 2, kt & 1);
+      load_v(kt, kt & 1);
+      const int rd = (kt + 1) & 1;
+      s_tile(rd, Sn0, Sn1);
+      pv_tile(rd, Pp, st);
+      softmax_tile<D, false>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
+      apply_rescale(st);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Pp[i] = Pc[i];
+      Sc0 = Sn0;
+      Sc1 = Sn1;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
   }
+  for (; kt < n_tiles; ++kt)
+    step(kt, kt + 1 < my_tiles, kt >= 1 && kt - 1 < my_tiles, kt < my_tiles, kt == my_tiles - 1);
+  // last P.V of waves whose diagonal is the workgroup's last tile
+  if (my_tiles == n_tiles && my_tiles > 0) pv_tile((n_tiles - 1) & 1, Pp, st);
 
   if (!wave_active) return;
   // ---- epilogue: out = bf16(O * (1/l)), lse = m + log(l) ----
-  const float lt = sum_halves(l_run);
+  const float lt = sum_halves(st.l_run);
   const float inv = 1.0f / lt;
   uint16_t* Og = a.out + base + (size_t)q * rs;
 #pragma unroll
@@ -227,11 +306,11 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * dt + 8 * g + 4 * h;
       u32x2 w;
-      w[0] = pack_bf16(O[dt][4 * g] * inv, O[dt][4 * g + 1] * inv);
-      w[1] = pack_bf16(O[dt][4 * g + 2] * inv, O[dt][4 * g + 3] * inv);
+      w[0] = pack_bf16(st.O[dt][4 * g] * inv, st.O[dt][4 * g + 1] * inv);
+      w[1] = pack_bf16(st.O[dt][4 * g + 2] * inv, st.O[dt][4 * g + 3] * inv);
       *(u32x2*)(Og + d0) = w;
     }
-  if (h == 0) a.lse[(size_t)pair * a.T + q] = m_run * su + logf(lt);
+  if (h == 0) a.lse[(size_t)pair * a.T + q] = st.m_use * su + logf(lt);
 }
 
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s) {
