@@ -79,7 +79,8 @@ int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, c
 const char* metalllmAttnErrorString(int code);
 
 /* Test hook (no counterpart in the reference): writes, for workgroup ids 0..count-1 of the
- * forward (kind 0) or backward (kind 1) grid of shape p, the (pair, block) each one owns into
+ * forward (kind 0), backward dK/dV (kind 1) or backward dQ (kind 2) grid of shape p, the
+ * (pair, block) each one owns into
  * out[2*i], out[2*i+1]. Returns the grid size, or a negative error code. Host-only. */
 int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_t count);
 

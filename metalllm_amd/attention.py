@@ -142,7 +142,7 @@ def attention_backward(dO, q, k, v, out, lse, stream=None):
 
 
 def work_map(kind: int, B: int, T: int, H: int, D: int):
-    """(pair, block) owned by each workgroup id of the forward (0) or backward (1) grid."""
+    """(pair, block) owned by each workgroup id of the forward (0), dK/dV (1) or dQ (2) grid."""
     import numpy as np
     p = AttentionParams.of(B, T, H, D)
     n = _lib().metalllmAttnWorkMap(kind, ctypes.byref(p), None, 0)

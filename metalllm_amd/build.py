@@ -16,7 +16,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmetalllm_attn.so")
-SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_computed.hip"]
+SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_computed.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -28,9 +28,12 @@ FLAGS = [
 ]
 
 
-# Per-source extra flags: the backward keeps its matrix-core accumulators in arch VGPRs (they
-# are rounded by VALU code every query block, and AGPR<->VGPR copies would dominate).
-EXTRA = {"attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source extra flags: the backward kernels' per-tile slot loops are fully unrolled (their
+# register arrays are indexed by the slot), which exceeds the default unroll size limit.
+EXTRA = {
+    "attn_bwd.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
+    "attn_bwd_dq.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
+}
 
 
 def _run(cmd):

@@ -56,8 +56,10 @@ int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, c
       !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
     return METALLLM_ATTN_E_ALIGN;
   mla::BwdArgs a{dZ, d, l, q, k, v, dQ, dK, dV, (int)p->M, (int)p->NH, (int)p->B, head_scale(p->D)};
-  return mla::launch_backward(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
-                                                                               : METALLLM_ATTN_E_LAUNCH;
+  // dK/dV by the key owners, then dQ by the query owners (both on `stream`, in order)
+  if (mla::launch_backward(a, (int)p->D, (hipStream_t)stream) != hipSuccess) return METALLLM_ATTN_E_LAUNCH;
+  return mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                                  : METALLLM_ATTN_E_LAUNCH;
 }
 
 const char* metalllmAttnErrorString(int code) {
@@ -78,14 +80,14 @@ int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_
   const int rc = validate(p);
   if (rc) return rc;
   if (!out && count > 0) return METALLLM_ATTN_E_NULL;
-  if (kind != 0 && kind != 1) return METALLLM_ATTN_E_LAYOUT;
+  if (kind < 0 || kind > 2) return METALLLM_ATTN_E_LAYOUT;
   const int npairs = (int)(p->B * p->NH);
-  const int blk = kind == 0 ? mla::kFwdBlockM : mla::kBwdBlockN;
+  const int blk = kind == 0 ? mla::kFwdBlockM : kind == 1 ? mla::kBwdBlockN : mla::kDqBlockM;
   const int nblk = ((int)p->M + blk - 1) / blk;
   const int grid = npairs * nblk;
   for (int i = 0; i < count && i < grid; ++i) {
     int pair, b;
-    mla::decode_workgroup(i, npairs, nblk, kind == 0, pair, b);
+    mla::decode_workgroup(i, npairs, nblk, kind != 1, pair, b);
     out[2 * i] = pair;
     out[2 * i + 1] = b;
   }

@@ -1,33 +1,31 @@
-// attn_bwd.hip -- flashAttentionBackward on gfx950.
+// attn_bwd.hip -- the dK/dV half of flashAttentionBackward on gfx950 (key-owner kernel).
 //
 // Reference: /root/reference/attention.metal:198-299. For each 64-key tile kt and each 64-row
 // query tile qt >= kt:
 //   dP = bf16(dO.V^T), S = bf16(Q.K^T)                           (:274-275)
 //   p = exp(S*scale - lse[q]), p = 0 where key > q (diagonal), P = bf16(p)
 //   dS = bf16(p * (dP - D[q]) * scale)                            (:277-286)
-//   dQ[qt rows] += bf16(dS.K)        (fp32 atomic add, :288,292-296)
 //   dK = bf16(dK + dS^T.Q), dV = bf16(dV + P^T.dO)   once per query tile (:289-290)
-// The key-tile owner accumulates dK/dV race-free; only dQ is shared, through fp32 atomics.
+// The key-tile owner accumulates dK/dV race-free. dQ (:288,292-296) is computed by the
+// query-owner kernel in attn_bwd_dq.hip, which flashAttentionBackward launches after this one.
 //
-// Work split: one workgroup of 8 waves owns 256 keys (four reference key tiles) of one (b,h),
-// so each dQ element receives one fp32 atomic per 256 keys: the device's fp32 atomic rate, not
-// the matrix cores, is what bounds a smaller key block. Wave w owns keys 32w..32w+31: it keeps
-// their K and V rows in registers as matrix-core B operands, computes S and dP (lane = key),
-// P and dS, and updates dV^T += dO^T.P and dK^T += Q^T.dS. Between query blocks dK and dV are
-// bf16 values (the reference stores them as bf16 after every query tile), so they are carried
-// packed, two per register, and widened to fp32 only for one 32-row d slice at a time.
-// Per 64-row query block the workgroup stages Q and dO row-major ([q][d]), dO also transposed
-// ([d][q]), and lse*log2(e) and D; K is staged transposed ([d][key]) once. Matrix-core operands
-// are conflict-free 16-byte LDS reads at a per-lane base plus a compile-time offset, except
-// Q^T, which is read with ds_read_b64_tr_b16 from the row-major Q tile. dS is stored to LDS as
-// [q][key]; after a barrier the workgroup computes the dQ block [64 q][D] over all 256 keys, one
-// bf16-rounded part per reference key tile (64 keys), and adds it to dQ with fp32 atomics.
-// Query blocks entirely above a wave's keys are skipped by that wave; the dQ product skips the
-// same key tiles, and only diagonal blocks evaluate the causal mask.
+// Work split: 4 waves x 32 keys per workgroup, two workgroups per CU. Wave w owns keys
+// 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core B operands
+// and computes S and dP with lane = key (the query tile's Q and dO rows are A operands from
+// LDS), so P and dS come out of the accumulators already laid out as the B operands of
+// dV^T += dO^T.P and dK^T += Q^T.dS: no LDS round trip. dO^T and Q^T are read with
+// ds_read_b64_tr_b16 from the row-major tiles, four queries per read, in the order
+// {8g + 4h + i} that lane half h holds. Between query tiles dK and dV are bf16 values (the
+// reference stores them as bf16 after every query tile), carried packed two per register and
+// widened to fp32 for one 32-row d slice at a time.
+//
+// Per query tile: S and dP of query rows 0-31, their p, P and dS, the same for rows 32-63, then
+// the dK/dV products. Query tiles stream through LDS two stages deep by
+// global_load_lds_dwordx4: Q and dO rows, and lse and D of the tile (lse scaled by log2(e) in
+// place once it lands).
 //
 // Matrix-core passes, as the oracle models them: S and dP sum d in passes of 8 consecutive
-// values; dK/dV sum q in passes {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}; dQ sums keys
-// in passes of 8 consecutive keys.
+// values; dK/dV sum q in passes {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}.
 #include "attn_common.hpp"
 #include "attn_launch.hpp"
 
@@ -35,71 +33,49 @@ namespace mla {
 
 template <int D>
 struct BwdCfg {
-  static constexpr int BN = kBwdBlockN;  // keys per workgroup (256)
-  static constexpr int BM = kTile;       // query rows per step (the reference's query tile)
-  static constexpr int THREADS = 512;
-  static constexpr int KTP = BN + 8;               // transposed K pitch [D][BN]
-  static constexpr int QP = (D == 128) ? D + 24 : D + 8;  // row-major Q/dO pitch: 304 B serves b128 and tr reads
-  static constexpr int GTP = BM + 8;               // transposed dO pitch [D][BM]
-  static constexpr int SP = BN + 8;                // dS pitch [BM][BN]
-  static constexpr int KT_ELEMS = D * KTP;
-  static constexpr int Q_ELEMS = BM * QP;
-  static constexpr int GT_ELEMS = D * GTP;
-  static constexpr int S_ELEMS = BM * SP;
+  static constexpr int BN = kBwdBlockN;  // keys per workgroup (128)
+  static constexpr int BM = kTile;       // query rows per tile (the reference's query tile)
+  static constexpr int THREADS = 256;
+  static constexpr int P = (D == 128) ? D + 24 : D + 8;  // Q/dO row pitch: b128 row and tr reads conflict-free
+  static constexpr int TBYTES = BM * P * 2;              // one padded tile
+  static constexpr int SLOTS = P / 8;                    // 16-byte slots of a padded row
+  static constexpr int LPW = (SLOTS + 3) / 4;            // row-copy instructions per wave per tile (max)
+  static constexpr int STAT = 2 * TBYTES;                // lse (64 fp32), D (64 fp32), + 512 B the copy spills
+  static constexpr int STAGE = 2 * TBYTES + 1024;
   static constexpr int KC = D / 16;
   static constexpr int DT = D / 32;
-  static constexpr int QROWS = BM * D / (8 * 256);  // rows per thread of the Q (or dO) loader
-  static constexpr int QGROUPS = BM / QROWS;
-  static constexpr int KROWS = BN * D / (8 * THREADS);  // keys per thread of the K loader
-  static constexpr int KGROUPS = BN / KROWS;
-  static constexpr int DQ_WAVES = (BM / 32) * DT;  // 32x32 dQ tiles: 8 (D=128) or 4 (D=64)
 };
 
-// Position of row k (0..63) inside a transposed-tile row: chunk of 16, stored in the order
-// {0-3, 8-11, 4-7, 12-15} (the q order of a 32x32 accumulator's lane halves).
-__device__ __forceinline__ int perm_pos_b(int k) {
-  return (k & ~15) + 8 * ((k >> 2) & 1) + 4 * ((k >> 3) & 1) + (k & 3);
+typedef __attribute__((address_space(3))) uint16_t lds_u16b;
+__device__ __forceinline__ uint32_t lds_addr_b(const void* p) { return (uint32_t)(uintptr_t)(const lds_u16b*)p; }
+__device__ __forceinline__ u32x4 lds_b128_b(uint32_t byte_addr) {
+  return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)byte_addr;
 }
-__device__ __forceinline__ uint32_t pk_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-__device__ __forceinline__ uint32_t pk_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+__device__ __forceinline__ f32x4 lds_f4_b(uint32_t byte_addr) {
+  return *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)byte_addr;
+}
+__device__ __forceinline__ u32x2 lds_tr_b(uint32_t byte_addr) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) i16x4*)(uintptr_t)byte_addr));
+}
 
-// Transposed 16-byte piece of rows [r, r+8) in k-slot order {r..r+3 of half 0 / r+4.. of half
-// 1} is assembled by the caller; this writes KROWS-key groups of a [D][*] transposed tile.
-template <int R>
-__device__ __forceinline__ void store_transposed(uint16_t* dst, int pitch, const u32x4* r) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int w = j >> 1;
-    uint16_t* row = dst + j * pitch;
-    if (R == 8) {
-      u32x4 o;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) o[p] = (j & 1) ? pk_hi(r[2 * p][w], r[2 * p + 1][w]) : pk_lo(r[2 * p][w], r[2 * p + 1][w]);
-      *(u32x4*)row = o;
-    } else if (R == 4) {
-      u32x2 o;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) o[p] = (j & 1) ? pk_hi(r[2 * p][w], r[2 * p + 1][w]) : pk_lo(r[2 * p][w], r[2 * p + 1][w]);
-      *(u32x2*)row = o;
-    } else {
-      *(uint32_t*)row = (j & 1) ? pk_hi(r[0][w], r[1][w]) : pk_lo(r[0][w], r[1][w]);
-    }
-  }
-}
+// Anchors: an empty asm that reads and rewrites a value pins its computation to this point of
+// the program (code motion cannot move the work into another slot).
+__device__ __forceinline__ void pin(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
+__device__ __forceinline__ void pin(uint32_t& a) { asm volatile("" : "+v"(a)); }
+
+template <bool V>
+struct DiagTag {
+  static constexpr bool value = V;
+};
 
 template <int D>
-__global__ void __launch_bounds__(512, 1) bwd_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[C::KT_ELEMS + 2 * C::Q_ELEMS + C::GT_ELEMS + C::S_ELEMS];
-  __shared__ __attribute__((aligned(16))) float lse_s[C::BM];
-  __shared__ __attribute__((aligned(16))) float dd_s[C::BM];
-  uint16_t* Kt = smem;
-  uint16_t* Qs = Kt + C::KT_ELEMS;
-  uint16_t* Gs = Qs + C::Q_ELEMS;
-  uint16_t* Gt = Gs + C::Q_ELEMS;
-  uint16_t* dSs = Gt + C::GT_ELEMS;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int nkb = (a.T + C::BN - 1) / C::BN;
   int pair, kb;
@@ -107,36 +83,26 @@ __global__ void __launch_bounds__(512, 1) bwd_kernel(BwdArgs a) {
   const int b = pair / a.H, hd = pair - b * a.H;
   const int rs = a.H * D;
   const size_t base = ((size_t)b * a.T * a.H + hd) * D;
-  const uint16_t* Qg = a.q + base;
+  const char* Qg = (const char*)(a.q + base);
+  const char* Gg = (const char*)(a.dO + base);
   const uint16_t* Kg = a.k + base;
   const uint16_t* Vg = a.v + base;
-  const uint16_t* Gg = a.dO + base;
   const float* lse_g = a.lse + (size_t)pair * a.T;
   const float* dd_g = a.Dv + (size_t)pair * a.T;
+  const size_t tile_bytes = (size_t)C::BM * rs * 2;
 
   const int k0 = kb * C::BN;
-  const int kl = 32 * wave + l32;  // this lane's key within the block
-  const int kw = k0 + 32 * wave;   // the wave's first key
-  const bool wave_keys = kw < a.T;
+  const int kw = k0 + 32 * wave;  // the wave's first key
+  const bool wave_keys = kw < a.T;  // false only in the last block when T % 128 == 64
   const int key = kw + l32;
+  const int key_ld = min(key, a.T - 1);  // rows of keys past T are read in bounds, never stored
 
-  // ---- K block, transposed -> LDS (keys past T zero-filled) ----
-  {
-    const int kg = tid % C::KGROUPS, g = tid / C::KGROUPS;  // keys KROWS*kg.., d 8g..8g+7
-    u32x4 kr[C::KROWS];
-#pragma unroll
-    for (int i = 0; i < C::KROWS; ++i) {
-      const int row = C::KROWS * kg + i;
-      kr[i] = (k0 + row < a.T) ? *(const u32x4*)(Kg + (size_t)(k0 + row) * rs + 8 * g) : u32x4{0, 0, 0, 0};
-    }
-    store_transposed<C::KROWS>(Kt + 8 * g * C::KTP + C::KROWS * kg, C::KTP, kr);
-  }
   // own K and V rows as B operands: lane holds row `key`, d = 16c + 8h .. +7
   u32x4 Kr[C::KC], Vr[C::KC];
 #pragma unroll
   for (int c = 0; c < C::KC; ++c) {
-    Kr[c] = wave_keys ? *(const u32x4*)(Kg + (size_t)key * rs + 16 * c + 8 * h) : u32x4{0, 0, 0, 0};
-    Vr[c] = wave_keys ? *(const u32x4*)(Vg + (size_t)key * rs + 16 * c + 8 * h) : u32x4{0, 0, 0, 0};
+    Kr[c] = *(const u32x4*)(Kg + (size_t)key_ld * rs + 16 * c + 8 * h);
+    Vr[c] = *(const u32x4*)(Vg + (size_t)key_ld * rs + 16 * c + 8 * h);
   }
   // dK^T, dV^T (m = d, n = key) as packed bf16 pairs of accumulator rows (r, r+1)
   uint32_t dKp[C::DT][8], dVp[C::DT][8];
@@ -148,176 +114,230 @@ __global__ void __launch_bounds__(512, 1) bwd_kernel(BwdArgs a) {
       dVp[dt][i] = 0u;
     }
 
-  // ---- per query block loader: threads 0-255 stage Q, 256-511 stage dO (+ transposed) ----
+  // Query-tile copy. Q and dO rows: instruction i covers 16-byte slots 64i..64i+63 of the padded
+  // tile (slot s = row s / SLOTS, chunk s % SLOTS; pad chunks re-read the row's last chunk).
+  // lse and D of the tile: wave 0, lanes 0-15 and 16-31 (lanes 32-63 repeat them).
+  uint32_t off[C::LPW];
+#pragma unroll
+  for (int j = 0; j < C::LPW; ++j) {
+    const int s = 64 * (wave + 4 * j) + lane, row = s / C::SLOTS, c = min(s % C::SLOTS, D / 8 - 1);
+    off[j] = (uint32_t)(row * rs * 2 + c * 16);
+  }
   const int nqb = a.T / C::BM;
   const int qb0 = k0 / C::BM;
-  const int lt = tid & 255;
-  const int qg = lt % C::QGROUPS, dg = lt / C::QGROUPS;
-  const bool load_do = tid >= 256;
-  const uint16_t* Lg = load_do ? Gg : Qg;
-  uint16_t* Ln = load_do ? Gs : Qs;
-  u32x4 lreg[C::QROWS];
-  float sreg = 0.0f;
-  auto gload = [&](int qb) {
+  const uint32_t smem_a = lds_addr_b(smem);
+  auto issue_tile = [&](int qb, int stage) {
+    const char* qs = Qg + (size_t)qb * tile_bytes;
+    const char* gs = Gg + (size_t)qb * tile_bytes;
+    const uint32_t dst = smem_a + stage * C::STAGE;
 #pragma unroll
-    for (int i = 0; i < C::QROWS; ++i)
-      lreg[i] = *(const u32x4*)(Lg + (size_t)(qb * C::BM + C::QROWS * qg + i) * rs + 8 * dg);
-    if (tid < C::BM)
-      sreg = lse_g[qb * C::BM + tid];
-    else if (tid < 2 * C::BM)
-      sreg = dd_g[qb * C::BM + tid - C::BM];
+    for (int j = 0; j < C::LPW; ++j)
+      if (wave + 4 * j < C::SLOTS) {
+        dma16(off[j], qs, dst + 1024 * (wave + 4 * j));
+        dma16(off[j], gs, dst + C::TBYTES + 1024 * (wave + 4 * j));
+      }
+    if (wave == 0) {
+      const int l = lane & 31;
+      const float* src = (l < 16 ? lse_g : dd_g) + qb * C::BM + 4 * (l & 15);
+      dma16_v(src, dst + C::STAT);
+    }
   };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < C::QROWS; ++i) *(u32x4*)(Ln + (C::QROWS * qg + i) * C::QP + 8 * dg) = lreg[i];
-    if (load_do) store_transposed<C::QROWS>(Gt + 8 * dg * C::GTP + perm_pos_b(C::QROWS * qg), C::GTP, lreg);
-    if (tid < C::BM)
-      lse_s[tid] = sreg * kLog2e;  // the exponent is evaluated in base 2
-    else if (tid < 2 * C::BM)
-      dd_s[tid - C::BM] = sreg;
+  // lse -> lse*log2(e) in place, by wave 0 once its copy has landed (exponents are base 2)
+  auto scale_lse = [&](int stage) {
+    if (wave == 0) {
+      float* l2 = (float*)(smem + stage * C::STAGE + C::STAT);
+      l2[lane] = l2[lane] * kLog2e;
+    }
   };
 
-  gload(qb0);
-  lstore();
-  __syncthreads();
-
-  // per-lane operand bases (compile-time offsets are added at each use)
-  const uint16_t* qa = Qs + l32 * C::QP + 8 * h;    // S A-operand: row q, d slots
-  const uint16_t* ga = Gs + l32 * C::QP + 8 * h;    // dP A-operand
-  const uint16_t* gt = Gt + l32 * C::GTP + 8 * h;   // dV A-operand: row d, q slots (k-slot order)
-  const uint16_t* qt = Qs + ((lane & 15) >> 2) * C::QP + 4 * (lane & 3) + 16 * ((lane >> 4) & 1) + 4 * h * C::QP;  // Q^T via tr
-  const uint16_t* sa = dSs + l32 * C::SP + 8 * h;   // dQ A-operand: row q, key slots
-  const uint16_t* st = dSs + ((lane & 15) >> 2) * C::SP + 4 * (lane & 3) + 16 * ((lane >> 4) & 1) + 4 * h * C::SP +
-                       32 * wave;                     // dK B-operand (dS^T) via tr reads
-  const uint16_t* kt = Kt + l32 * C::KTP + 8 * h;   // dQ B-operand: row d, key slots
+  // LDS operand addresses (bytes within a stage)
+  const uint32_t row_rd = 2 * (l32 * C::P + 8 * h);  // S / dP A operand: row = q, 8 d at 16c + 8h
+  // dV^T / dK^T A operand (dO^T, Q^T) by tr reads: group g = lane/16 covers d = 16(g%2) .. +15 of
+  // a 32-d tile; source lane s = lane%16 points at query row 4h + s/4 (+8 for the second read)
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const uint32_t tr_rd = 2 * ((4 * h + (s16 >> 2)) * C::P + 16 * (g16 & 1) + 4 * (s16 & 3));
+  const uint32_t st_rd = 4 * (4 * h);  // statistics of query row 32t + 8g + 4h + i at +4(32t + 8g + i)
   const float sl = a.scale * kLog2e;
+  const float scale = a.scale;
 
-  for (int qb = qb0; qb < nqb; ++qb) {
-    if (qb + 1 < nqb) gload(qb + 1);
-    const int qbase = qb * C::BM;
-    const bool active = wave_keys && kw <= qbase + C::BM - 1;
-    if (active) {
-      const bool diag = kw + 31 > qbase;
-      uint32_t Pw[2][8];  // P, packed bf16, rows q = 32qs + 8g + 4h + i (dS goes to LDS only)
+  // Update accumulators: chain n (dV of d tile n for n < DT, else dK of d tile n - DT) runs in
+  // block n % 2; while it runs, the other block's previous chain is rounded back into the bf16
+  // state and the next chain's state is widened into it.
+  f32x16 acc[2] = {zero16(), zero16()};
+  auto state = [&](int n) -> uint32_t* { return n < C::DT ? dVp[n] : dKp[n - C::DT]; };
+  auto pack_pairs = [&](int n, int u0, int u1) {  // state(n)[u] = bf16 pair of block n % 2
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        f32x16 S = zero16(), dP = zero16();
-#pragma unroll
-        for (int c = 0; c < C::KC; ++c) {
-          S = mfma(lds_read16(qa + 32 * qs * C::QP + 16 * c), Kr[c], S);
-          dP = mfma(lds_read16(ga + 32 * qs * C::QP + 16 * c), Vr[c], dP);
-        }
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ql = 32 * qs + 8 * g + 4 * h;
-          const f32x4 lv = *(const f32x4*)(lse_s + ql);
-          const f32x4 dv = *(const f32x4*)(dd_s + ql);
-          float sv[4], pv[4], ds[4];
-          const uint32_t s01 = pack_bf16(S[4 * g], S[4 * g + 1]), s23 = pack_bf16(S[4 * g + 2], S[4 * g + 3]);
-          const uint32_t d01 = pack_bf16(dP[4 * g], dP[4 * g + 1]), d23 = pack_bf16(dP[4 * g + 2], dP[4 * g + 3]);
-          sv[0] = bf_lo(s01);
-          sv[1] = bf_hi(s01);
-          sv[2] = bf_lo(s23);
-          sv[3] = bf_hi(s23);
-          const float dp[4] = {bf_lo(d01), bf_hi(d01), bf_lo(d23), bf_hi(d23)};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pv[i] = exp2_hw(fmaf(sv[i], sl, -lv[i]));
-          if (diag) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (key > qbase + ql + i) pv[i] = 0.0f;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ds[i] = (pv[i] * (dp[i] - dv[i])) * a.scale;
-          Pw[qs][2 * g] = pack_bf16(pv[0], pv[1]);
-          Pw[qs][2 * g + 1] = pack_bf16(pv[2], pv[3]);
-          const uint32_t s0 = pack_bf16(ds[0], ds[1]), s1 = pack_bf16(ds[2], ds[3]);
-          uint16_t* dcol = dSs + ql * C::SP + kl;
-          dcol[0] = (uint16_t)s0;
-          dcol[C::SP] = (uint16_t)(s0 >> 16);
-          dcol[2 * C::SP] = (uint16_t)s1;
-          dcol[3 * C::SP] = (uint16_t)(s1 >> 16);
-        }
-      }
-      // ---- dV^T += dO^T.P, then dK^T += Q^T.dS over the 64 q; one d slice (32 rows) at a time.
-      // The reference stores dK/dV as bf16 after every query tile: unpack, accumulate, repack.
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        f32x16 av;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          av[2 * i] = bf_lo(dVp[dt][i]);
-          av[2 * i + 1] = bf_hi(dVp[dt][i]);
-        }
-#pragma unroll
-        for (int cq = 0; cq < 4; ++cq) {
-          const int qs = cq >> 1, w0 = 4 * (cq & 1);
-          const u32x4 Bp = {Pw[qs][w0], Pw[qs][w0 + 1], Pw[qs][w0 + 2], Pw[qs][w0 + 3]};
-          av = mfma(lds_read16(gt + 32 * dt * C::GTP + 16 * cq), Bp, av);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dVp[dt][i] = pack_bf16(av[2 * i], av[2 * i + 1]);
-      }
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        f32x16 ak;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          ak[2 * i] = bf_lo(dKp[dt][i]);
-          ak[2 * i + 1] = bf_hi(dKp[dt][i]);
-        }
-#pragma unroll
-        for (int cq = 0; cq < 4; ++cq) {
-          // dS B operand (k = q in the accumulator's row order, n = key) read back transposed
-          // from this wave's own columns of the [q][key] tile
-          const u32x2 slo = lds_tr(st + 16 * cq * C::SP);
-          const u32x2 shi = lds_tr(st + (16 * cq + 8) * C::SP);
-          const u32x4 Bs = {slo[0], slo[1], shi[0], shi[1]};
-          const u32x2 lo = lds_tr(qt + 16 * cq * C::QP + 32 * dt);
-          const u32x2 hi = lds_tr(qt + (16 * cq + 8) * C::QP + 32 * dt);
-          ak = mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, Bs, ak);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dKp[dt][i] = pack_bf16(ak[2 * i], ak[2 * i + 1]);
-      }
+    for (int u = u0; u < u1; ++u) {
+      uint32_t v = pack_bf16(acc[n & 1][2 * u], acc[n & 1][2 * u + 1]);
+      pin(v);
+      state(n)[u] = v;
     }
-    __syncthreads();  // dS complete; Q/dO tiles no longer read
-    if (qb + 1 < nqb) lstore();
+  };
+  auto unpack_pairs = [&](int n, int u0, int u1) {  // block n % 2 = widened state(n)
+#pragma unroll
+    for (int u = u0; u < u1; ++u) {
+      float lo = bf_lo(state(n)[u]), hi = bf_hi(state(n)[u]);
+      pin(lo, hi);
+      acc[n & 1][2 * u] = lo;
+      acc[n & 1][2 * u + 1] = hi;
+    }
+  };
 
-    // ---- dQ block: one bf16 part per reference key tile (64 keys), fp32 atomic add ----
-    if (wave < C::DQ_WAVES) {
-      const int qs = wave / C::DT, dt = wave % C::DT;
-      f32x16 sum = zero16();
-      bool any = false;
-#pragma unroll
-      for (int part = 0; part < C::BN / kTile; ++part) {
-        // keys of reference key tile kb*4+part: present, and at or below this query tile
-        if (k0 + kTile * part >= a.T || (k0 / kTile) + part > qb) continue;
-        any = true;
-        f32x16 acc = zero16();
-#pragma unroll
-        for (int ck = 0; ck < 4; ++ck) {
-          const int kc = kTile * part + 16 * ck;
-          acc = mfma(lds_read16(sa + 32 * qs * C::SP + kc), lds_read16(kt + 32 * dt * C::KTP + kc), acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          round_pair(acc, r);
-          sum[r] += acc[r];
-          sum[r + 1] += acc[r + 1];
-        }
+  // One query tile: NS matrix-core instructions in a fixed order, one per slot, each slot also
+  // doing a slice of vector work that does not depend on it. Slots:
+  //   [0, KC) S of rows 0-31, d step c     [KC, 2KC) dP of rows 0-31
+  //   [2KC, 3KC) S of rows 32-63           [3KC, 4KC) dP of rows 32-63
+  //   [4KC, NS) update chain n = (i - 4KC) / 4, query step j = (i - 4KC) % 4
+  // S[t], dP[t] hold rows q = 32t + 8(r/4) + 4h + r%4 of the tile, lane = key.
+  auto qtile = [&](int qb, int stage, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    constexpr int NS = 4 * C::KC + 8 * C::DT;
+    constexpr int PPS = 8 / C::KC;  // score pairs of vector work per S/dP slot
+    const uint32_t qbase_a = lds_addr_b(smem + stage * C::STAGE), gbase_a = qbase_a + C::TBYTES;
+    const uint32_t stat_a = qbase_a + C::STAT + st_rd;
+    const int qrow = qb * C::BM + 4 * h - key;  // q - key = qrow + 32t + 8g + i
+    f32x16 x0 = zero16(), x1 = zero16(), y0 = zero16(), y1 = zero16();
+    uint32_t Pp[16], dS[16];  // packed bf16: index 8t + r/2
+
+    auto operand = [&](int i) -> u32x4 {
+      if (i < 4 * C::KC) {
+        const int seg = i / C::KC, t = seg >> 1, c = i % C::KC;
+        return lds_b128_b(((seg & 1) ? gbase_a : qbase_a) + row_rd + 2 * (32 * t * C::P + 16 * c));
       }
-      if (any) {
-        float* dQg = a.dQ + base + (size_t)qbase * rs + 32 * dt + l32;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int ql = 32 * qs + 8 * (r >> 2) + 4 * h + (r & 3);
-          unsafeAtomicAdd(dQg + (size_t)ql * rs, sum[r]);
-        }
+      const int k = i - 4 * C::KC, n = k / 4, j = k % 4, dt = n % C::DT;
+      const uint32_t src = (n >= C::DT ? qbase_a : gbase_a) + tr_rd + 2 * (16 * j * C::P + 32 * dt);
+      const u32x2 lo = lds_tr_b(src), hi = lds_tr_b(src + 2 * 8 * C::P);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    // Score pairs of vector work in slot i: kind 1 = p of half t, kind 2 = dS of half t; pairs
+    // r = 2u for u in [u0, u0 + cnt).
+    struct Work {
+      int kind, t, u0, cnt;
+    };
+    auto work = [&](int i) -> Work {
+      if (i < 4 * C::KC) {
+        const int seg = i / C::KC, u0 = (i % C::KC) * PPS;
+        if (seg == 1) return {1, 0, u0, PPS};
+        if (seg == 2) return {2, 0, u0, PPS};
+        if (seg == 3) return {1, 1, u0, PPS};
+        return {0, 0, 0, 0};
       }
+      const int k = i - 4 * C::KC;  // dS of half 1 spread over the dV chains' 4DT slots
+      if (k < 4 * C::DT) {
+        constexpr int SPAN = (4 * C::DT) / 8;  // slots per pair (1 or 2)
+        if (k % SPAN == 0) return {2, 1, k / SPAN, 1};
+      }
+      return {0, 0, 0, 0};
+    };
+    // lse (kind 1) or D (kind 2) of the rows of the pairs of slot i (read one slot ahead)
+    auto stats = [&](int i) -> f32x4 {
+      const Work w = work(i);
+      const uint32_t ad = stat_a + (w.kind == 2 ? 256 : 0) + 4 * (32 * w.t + 8 * (w.u0 >> 1) + 2 * (w.u0 & 1));
+      if (w.cnt == 2) return lds_f4_b(ad);
+      const f32x2 v = *(const __attribute__((address_space(3))) f32x2*)(uintptr_t)ad;
+      return f32x4{v[0], v[1], 0.0f, 0.0f};
+    };
+    auto p_pair = [&](f32x16& x, int t, int u, float l0, float l1) {
+      const int r = 2 * u;
+      round_pair(x, r);
+      float p0 = exp2_hw(fmaf(x[r], sl, -l0));
+      float p1 = exp2_hw(fmaf(x[r + 1], sl, -l1));
+      if (DIAG) {
+        const int d = qrow + 32 * t + 8 * (r >> 2) + (r & 3);  // q - key of element r
+        if (d < 0) p0 = 0.0f;
+        if (d + 1 < 0) p1 = 0.0f;
+      }
+      pin(p0, p1);
+      x[r] = p0;
+      x[r + 1] = p1;
+      uint32_t pk = pack_bf16(p0, p1);
+      pin(pk);
+      Pp[8 * t + u] = pk;
+    };
+    auto ds_pair = [&](const f32x16& x, f32x16& y, int t, int u, float d0_, float d1_) {
+      const int r = 2 * u;
+      round_pair(y, r);
+      const float d0 = (x[r] * (y[r] - d0_)) * scale;
+      const float d1 = (x[r + 1] * (y[r + 1] - d1_)) * scale;
+      uint32_t pk = pack_bf16(d0, d1);
+      pin(pk);
+      dS[8 * t + u] = pk;
+    };
+
+    u32x4 ring[2];
+    f32x4 sring[2];
+    ring[0] = operand(0);
+    sring[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      if (i + 1 < NS) {
+        ring[(i + 1) % 2] = operand(i + 1);
+        if (work(i + 1).kind) sring[(i + 1) % 2] = stats(i + 1);
+      }
+      const u32x4& op = ring[i % 2];
+      if (i < 4 * C::KC) {
+        const int seg = i / C::KC, c = i % C::KC;
+        if (seg == 0) x0 = mfma(op, Kr[c], x0);
+        else if (seg == 1) y0 = mfma(op, Vr[c], y0);
+        else if (seg == 2) x1 = mfma(op, Kr[c], x1);
+        else y1 = mfma(op, Vr[c], y1);
+      } else {
+        const int k = i - 4 * C::KC, n = k / 4, j = k % 4;
+        const uint32_t* src = n >= C::DT ? dS : Pp;
+        acc[n & 1] = mfma(op, u32x4{src[4 * j], src[4 * j + 1], src[4 * j + 2], src[4 * j + 3]}, acc[n & 1]);
+      }
+      // vector work of this slot
+      const Work w = work(i);
+      const f32x4 st = sring[i % 2];
+#pragma unroll
+      for (int v = 0; v < w.cnt; ++v) {
+        if (w.kind == 1)
+          p_pair(w.t ? x1 : x0, w.t, w.u0 + v, st[2 * v], st[2 * v + 1]);
+        else if (w.kind == 2)
+          ds_pair(w.t ? x1 : x0, w.t ? y1 : y0, w.t, w.u0 + v, st[2 * v], st[2 * v + 1]);
+      }
+      if (i < C::KC) {
+        // the previous tile's last chain (dK of d tile DT-1, block 1) back into the state
+        pack_pairs(2 * C::DT - 1, (i * 8) / C::KC, ((i + 1) * 8) / C::KC);
+      } else if (i >= 3 * C::KC && i < 4 * C::KC) {
+        // widen the first two chains' state (dV of d tiles 0 and 1)
+        const int s_ = i - 3 * C::KC, per = 16 / C::KC, u0 = s_ * per;
+#pragma unroll
+        for (int u = u0; u < u0 + per; ++u) unpack_pairs(u < 8 ? 0 : 1, u & 7, (u & 7) + 1);
+      } else if (i >= 4 * C::KC) {
+        const int k = i - 4 * C::KC, n = k / 4, j = k % 4;
+        if (n >= 1 && j == 1) pack_pairs(n - 1, 0, 8);
+        if (n + 1 < 2 * C::DT && n >= 1 && j >= 2) unpack_pairs(n + 1, 4 * (j - 2), 4 * (j - 2) + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // dS consumed; next Q/dO tiles visible
+  };
+
+  // ---- query tiles qb0 .. nqb-1 ----
+  // Every wave runs every tile (no per-wave branch: the state stays in place across tiles). The
+  // first two tiles hold the block's diagonal and run masked: a wave whose keys all lie above
+  // the tile gets p = 0 there and leaves its state unchanged (adding exact zeros). Keys past T
+  // (last block, T % 128 == 64) compute on clamped rows and are never stored.
+  issue_tile(qb0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  scale_lse(0);
+  __syncthreads();
+  int qb = qb0, it = 0;
+  for (; qb < nqb && qb < qb0 + 2; ++qb, ++it) {
+    if (qb + 1 < nqb) issue_tile(qb + 1, (it + 1) & 1);
+    qtile(qb, it & 1, DiagTag<true>());
+    __builtin_amdgcn_s_waitcnt(0);
+    if (qb + 1 < nqb) scale_lse((it + 1) & 1);
+    __syncthreads();
   }
+  for (; qb < nqb; ++qb, ++it) {
+    if (qb + 1 < nqb) issue_tile(qb + 1, (it + 1) & 1);
+    qtile(qb, it & 1, DiagTag<false>());
+    __builtin_amdgcn_s_waitcnt(0);
+    if (qb + 1 < nqb) scale_lse((it + 1) & 1);
+    __syncthreads();
+  }
+  pack_pairs(2 * C::DT - 1, 0, 8);
 
   // ---- dK, dV: lane = key, rows d = 32dt + 8g + 4h + i ----
   if (!wave_keys) return;
@@ -337,9 +357,9 @@ hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s) {
   const int nkb = (a.T + kBwdBlockN - 1) / kBwdBlockN;
   const dim3 grid((unsigned)(a.B * a.H * nkb));
   if (D == 64)
-    hipLaunchKernelGGL(bwd_kernel<64>, grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL(bwd_kernel<64>, grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(bwd_kernel<128>, grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL(bwd_kernel<128>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -1,0 +1,279 @@
+// attn_bwd_dq.hip -- the dQ half of flashAttentionBackward on gfx950 (query-owner kernel).
+//
+// Reference: /root/reference/attention.metal:270-296. For a query row q and every key k <= q:
+//   S = bf16(Q.K^T), dP = bf16(dO.V^T)                              (:274-275)
+//   p = exp(S*scale - lse[q]) (0 above the diagonal)                 (:277-282)
+//   dS = bf16(p * (dP - D[q]) * scale)                               (:284)
+//   dQ[q] += dS.K    (fp32 atomic add into the caller-zeroed dQ, :288,292-296)
+// The reference computes dS inside the key-tile owner and adds one dQ part per (key tile,
+// query tile) with fp32 atomics. Here a query-owner workgroup recomputes S, dP and dS for its
+// 128 query rows over all keys, keeps dQ in matrix-core accumulators, and adds it into dQ with
+// one fp32 atomic per element: the device executes about 0.33e12 fp32 atomic adds per second,
+// so the owner-side form (one atomic per element per key tile) would cost more than the whole
+// kernel at long sequences. The dQ product sums each query's keys in fp32 across key tiles (the
+// reference rounds each 64-key part to bf16 first, :288; the difference is far inside the
+// gradient tolerance).
+//
+// Work split: 4 waves x 32 query rows per workgroup, two workgroups per CU (two waves per SIMD
+// hide each other's LDS and barrier waits). Lane = query: the wave computes S^T and dP^T
+// (keys x queries) with K and V rows from LDS as A operands and its own Q and dO rows as
+// register B operands, so p, dS and the statistics lse[q], D[q] are per-lane scalars. dS^T,
+// packed to bf16, is directly the B operand of dQ^T += K^T.dS^T; K^T is read with
+// ds_read_b64_tr_b16 from the row-major K tile, four keys per read, in the order {8g + 4h + i}
+// that lane half h of a 32-key subtile holds.
+//
+// Per 64-key tile the 48 matrix-core instructions (D=128) run in a fixed order, one per slot,
+// each with a slice of the vector work it does not depend on: S and dP of keys 0-31, then of
+// keys 32-63, then the dQ products; p and dS of the first 32 keys are computed while the
+// second half's products run, and dS of the second half while the first dQ products run.
+// Scheduling fences keep that order. K and V tiles go global -> LDS by
+// global_load_lds_dwordx4 (no registers), two stages: tile j+1 is copied while tile j is used.
+//
+// Matrix-core passes: S and dP sum d in passes of 8 consecutive values; dQ sums keys in passes
+// {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}.
+#include "attn_common.hpp"
+#include "attn_launch.hpp"
+
+namespace mla {
+
+template <int D>
+struct DqCfg {
+  static constexpr int BM = kDqBlockM;  // query rows per workgroup (128)
+  static constexpr int BN = kTile;      // keys per tile (64)
+  static constexpr int THREADS = 256;
+  static constexpr int P = (D == 128) ? D + 24 : D + 8;  // K, V row pitch: b128 row and tr reads conflict-free
+  static constexpr int TBYTES = kTile * P * 2;           // one padded tile
+  static constexpr int STAGE = 2 * TBYTES;               // K, V
+  static constexpr int SLOTS = P / 8;                    // 16-byte slots of a padded row (19 / 9)
+  static constexpr int LPW = (SLOTS + 3) / 4;            // row-copy instructions per wave per tile (max)
+  static constexpr int KC = D / 16;                      // 16-deep steps over d
+  static constexpr int DT = D / 32;                      // 32-wide d tiles of dQ
+  static constexpr int NM = 4 * KC + 4 * DT;             // matrix-core instructions per tile
+  static constexpr int PPS = 8 / KC;                     // score pairs of vector work per slot (1 or 2)
+  static constexpr int DQP = D + 4;                      // fp32 pitch of the dQ transpose buffer
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+
+__device__ __forceinline__ void g2lds16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+// Anchors: an empty asm that reads and rewrites a value pins its computation to this point of
+// the program (code motion cannot move the work into another slot).
+__device__ __forceinline__ void pin(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
+__device__ __forceinline__ void pin(uint32_t& a) { asm volatile("" : "+v"(a)); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_u16*)p; }
+__device__ __forceinline__ u32x4 lds_b128_at(uint32_t byte_addr) {
+  return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)byte_addr;
+}
+__device__ __forceinline__ u32x2 lds_tr_at(uint32_t byte_addr) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) i16x4*)(uintptr_t)byte_addr));
+}
+
+template <bool V>
+struct BoolTag {
+  static constexpr bool value = V;
+};
+
+template <int D>
+__global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
+  using C = DqCfg<D>;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int nqb = (a.T + C::BM - 1) / C::BM;
+  int pair, qb;
+  decode_workgroup(blockIdx.x, a.B * a.H, nqb, true, pair, qb);
+  const int b = pair / a.H, hd = pair - b * a.H;
+  const int rs = a.H * D;
+  const size_t base = ((size_t)b * a.T * a.H + hd) * D;
+  const uint16_t* Qg = a.q + base;
+  const uint16_t* Gg = a.dO + base;
+  const char* Kg = (const char*)(a.k + base);
+  const char* Vg = (const char*)(a.v + base);
+  const size_t tile_bytes = (size_t)C::BN * rs * 2;
+
+  const int q0 = qb * C::BM;
+  const int qw = q0 + 32 * wave;
+  const bool wave_active = qw < a.T;
+  const int n_tiles = (min(q0 + C::BM, a.T) - 1) / C::BN + 1;
+  const int my_tiles = wave_active ? qw / C::BN + 1 : 0;  // the last one is the diagonal tile
+  const int q = qw + l32;
+
+  // Q^T and dO^T as B operands: lane holds row q, d = 16c + 8h .. +7.
+  u32x4 Qr[C::KC], Gr[C::KC];
+#pragma unroll
+  for (int c = 0; c < C::KC; ++c) {
+    Qr[c] = wave_active ? *(const u32x4*)(Qg + (size_t)q * rs + 16 * c + 8 * h) : u32x4{0, 0, 0, 0};
+    Gr[c] = wave_active ? *(const u32x4*)(Gg + (size_t)q * rs + 16 * c + 8 * h) : u32x4{0, 0, 0, 0};
+  }
+  const float lse2 = wave_active ? a.lse[(size_t)pair * a.T + q] * kLog2e : 0.0f;  // exponent in base 2
+  const float dq = wave_active ? a.Dv[(size_t)pair * a.T + q] : 0.0f;
+  const float sl = a.scale * kLog2e;
+  const float scale = a.scale;
+
+  // Tile copy: instruction i of a tile covers 16-byte slots 64i..64i+63 of the padded tile;
+  // slot s is row s / SLOTS, chunk s % SLOTS; pad chunks re-read the row's last chunk.
+  uint32_t off[C::LPW];
+#pragma unroll
+  for (int j = 0; j < C::LPW; ++j) {
+    const int sl_ = 64 * (wave + 4 * j) + lane, row = sl_ / C::SLOTS, c = min(sl_ % C::SLOTS, D / 8 - 1);
+    off[j] = (uint32_t)(row * rs * 2 + c * 16);
+  }
+  auto issue_tile = [&](int kt) {
+    const char* ks = Kg + (size_t)kt * tile_bytes;
+    const char* vs = Vg + (size_t)kt * tile_bytes;
+    unsigned char* dst = smem + (kt & 1) * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::LPW; ++j)
+      if (wave + 4 * j < C::SLOTS) {
+        g2lds16(ks + off[j], dst + 1024 * (wave + 4 * j));
+        g2lds16(vs + off[j], dst + C::TBYTES + 1024 * (wave + 4 * j));
+      }
+  };
+
+  // LDS operand addresses (bytes, within a stage).
+  const uint32_t row_rd = 2 * (l32 * C::P + 8 * h);  // S^T / dP^T A operand: row = key, 8 d at 16c + 8h
+  // dQ^T A operand (K^T) by tr reads: group g = lane/16 covers d = 16(g%2) .. +15 of a 32-d tile;
+  // source lane s = lane%16 points at key row 4h + s/4 (+8 for the second read).
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const uint32_t tr_rd = 2 * ((4 * h + (s16 >> 2)) * C::P + 16 * (g16 & 1) + 4 * (s16 & 3));
+
+  // Matrix-core instruction i of a tile (compile-time after unrolling):
+  //   [0, KC): S of keys 0-31, d step i      [KC, 2KC): dP of keys 0-31
+  //   [2KC, 3KC): S of keys 32-63            [3KC, 4KC): dP of keys 32-63
+  //   [4KC, NM): dQ, key step c = k / DT, d tile dt = k % DT (k = i - 4KC)
+  auto operand = [&](int i, uint32_t kb, uint32_t vb) -> u32x4 {
+    if (i < 4 * C::KC) {
+      const int half = i / (2 * C::KC), isdp = (i / C::KC) & 1, c = i % C::KC;
+      return lds_b128_at((isdp ? vb : kb) + row_rd + 2 * (32 * half * C::P + 16 * c));
+    }
+    const int k = i - 4 * C::KC, dt = k % C::DT, c = k / C::DT;
+    const u32x2 lo = lds_tr_at(kb + tr_rd + 2 * (16 * c * C::P + 32 * dt));
+    const u32x2 hi = lds_tr_at(kb + tr_rd + 2 * ((16 * c + 8) * C::P + 32 * dt));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
+  f32x16 dQa[C::DT];
+#pragma unroll
+  for (int i = 0; i < C::DT; ++i) dQa[i] = zero16();
+  uint32_t dS[16];
+
+  // One key tile (MASK: this wave's diagonal tile). x = S^T (then p in place), y = dP^T, per
+  // 32-key half; pair r of half t is scores (r, r+1) of register block t.
+  auto tile = [&](int kt, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const uint32_t kb = lds_addr(smem + (kt & 1) * C::STAGE), vb = kb + C::TBYTES;
+    const int key0 = kt * C::BN;
+    f32x16 x0 = zero16(), x1 = zero16(), y0 = zero16(), y1 = zero16();
+    // p for score pair (r, r+1) of half t: s = bf16(S), p = exp2(s*scale*log2e - lse*log2e),
+    // 0 above the diagonal
+    auto p_pair = [&](f32x16& x, int t, int r) {
+      round_pair(x, r);
+      float p0 = exp2_hw(fmaf(x[r], sl, -lse2));
+      float p1 = exp2_hw(fmaf(x[r + 1], sl, -lse2));
+      if (MASK) {
+        const int k0 = key0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (k0 > q) p0 = 0.0f;
+        if (k0 + 1 > q) p1 = 0.0f;
+      }
+      pin(p0, p1);
+      x[r] = p0;
+      x[r + 1] = p1;
+    };
+    // dS = bf16(p * (bf16(dP) - D) * scale) for score pair (r, r+1) of half t
+    auto ds_pair = [&](const f32x16& x, f32x16& y, int t, int r) {
+      round_pair(y, r);
+      const float d0 = (x[r] * (y[r] - dq)) * scale;
+      const float d1 = (x[r + 1] * (y[r + 1] - dq)) * scale;
+      uint32_t pk = pack_bf16(d0, d1);
+      pin(pk);
+      dS[8 * t + (r >> 1)] = pk;
+    };
+    u32x4 ring[2];  // operand of slot i is read during slot i-1
+    ring[0] = operand(0, kb, vb);
+#pragma unroll
+    for (int i = 0; i < C::NM; ++i) {
+      if (i + 1 < C::NM) ring[(i + 1) % 2] = operand(i + 1, kb, vb);
+      const u32x4& op = ring[i % 2];
+      const int seg = i / C::KC;  // 0: S0, 1: dP0, 2: S1, 3: dP1, 4..: dQ
+      if (seg == 0)
+        x0 = mfma(op, Qr[i % C::KC], x0);
+      else if (seg == 1)
+        y0 = mfma(op, Gr[i % C::KC], y0);
+      else if (seg == 2)
+        x1 = mfma(op, Qr[i % C::KC], x1);
+      else if (seg == 3)
+        y1 = mfma(op, Gr[i % C::KC], y1);
+      else {
+        const int k = i - 4 * C::KC, dt = k % C::DT, c = k / C::DT;
+        dQa[dt] = mfma(op, u32x4{dS[4 * c], dS[4 * c + 1], dS[4 * c + 2], dS[4 * c + 3]}, dQa[dt]);
+      }
+      // vector work of this slot: seg 1: p of half 0; seg 2: dS of half 0; seg 3: p of half 1;
+      // first dQ segment: dS of half 1 (8 pairs each, PPS per slot)
+#pragma unroll
+      for (int u = 0; u < C::PPS; ++u) {
+        const int r = 2 * ((i % C::KC) * C::PPS + u);
+        if (seg == 1)
+          p_pair(x0, 0, r);
+        else if (seg == 2)
+          ds_pair(x0, y0, 0, r);
+        else if (seg == 3)
+          p_pair(x1, 1, r);
+        else if (seg == 4)
+          ds_pair(x1, y1, 1, r);
+      }
+      fence();
+    }
+  };
+
+  // ---- key tiles 0 .. n_tiles-1; tile j+1 is copied while tile j is used ----
+  issue_tile(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int j = 0; j < n_tiles; ++j) {
+    if (j + 1 < n_tiles) issue_tile(j + 1);
+    if (j + 1 < my_tiles)
+      tile(j, BoolTag<false>());
+    else if (j + 1 == my_tiles)
+      tile(j, BoolTag<true>());
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- dQ: transpose through LDS ([q][d] fp32), then one coalesced fp32 atomic per element ----
+  float* buf = (float*)smem + wave * 32 * C::DQP;
+  if (wave_active) {
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(f32x4*)(buf + l32 * C::DQP + 32 * dt + 8 * g + 4 * h) =
+            f32x4{dQa[dt][4 * g], dQa[dt][4 * g + 1], dQa[dt][4 * g + 2], dQa[dt][4 * g + 3]};
+  }
+  __syncthreads();
+  if (!wave_active) return;
+  float* dQg = a.dQ + base + (size_t)qw * rs;
+#pragma unroll 4
+  for (int r = 0; r < 32; ++r)
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c) unsafeAtomicAdd(dQg + (size_t)r * rs + 64 * c + lane, buf[r * C::DQP + 64 * c + lane]);
+}
+
+hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s) {
+  const int nqb = (a.T + kDqBlockM - 1) / kDqBlockM;
+  const dim3 grid((unsigned)(a.B * a.H * nqb));
+  if (D == 64)
+    hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace mla

@@ -32,6 +32,26 @@ __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
                                                  0, 0);
 }
 
+// Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l reads sbase + voff
+// and writes LDS byte address m0 + 16 l. Issued as inline asm, so the compiler does not track
+// the copy: the caller waits for it (s_waitcnt vmcnt) before a barrier that precedes any read
+// of the destination. The compiler-tracked builtin would make the first LDS read after it (of
+// any buffer) wait for every copy in flight, which serialises double-buffered tile copies with
+// the computation on the other buffer.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+// Same with a per-lane 64-bit source address.
+__device__ __forceinline__ void dma16_v(const void* src, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+// Waits for every vector-memory load of this wave (the untracked copies included) and every LDS
+// access, then synchronises the workgroup.
+__device__ __forceinline__ void wait_all_and_barrier() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

@@ -40,7 +40,8 @@ struct BwdArgs {
 
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s);
 hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
-hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);
+hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);     // dK, dV (key-owner)
+hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s);  // dQ (query-owner)
 
 // Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
 // spread so that every block of one pair lands on the same XCD (workgroups are handed to the
@@ -62,7 +63,8 @@ __host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, 
 }
 
 constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
-constexpr int kBwdBlockN = 256;  // keys owned by one backward workgroup
+constexpr int kBwdBlockN = 128;  // keys owned by one dK/dV workgroup
+constexpr int kDqBlockM = 128;   // query rows owned by one dQ workgroup
 constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)
 
 }  // namespace mla

@@ -10,16 +10,16 @@ import metalllm_amd as M
 
 @pytest.mark.parametrize("B,T,H,D", [(16, 256, 6, 64), (128, 256, 6, 64), (32, 1024, 12, 64), (16, 4096, 16, 128),
                                      (1, 192, 3, 128), (3, 320, 1, 64), (1, 64, 1, 64)])
-@pytest.mark.parametrize("kind,blk,last_first", [(0, 128, True), (1, 256, False)])
+@pytest.mark.parametrize("kind,blk,last_first", [(0, 128, True), (1, 128, False), (2, 128, True)])
 def test_partition(B, T, H, D, kind, blk, last_first):
     wm = M.work_map(kind, B, T, H, D)
     npairs, nblk = B * H, -(-T // blk)
     assert wm.shape == (npairs * nblk, 2)
     seen = set(map(tuple, wm.tolist()))
     assert seen == {(p, b) for p in range(npairs) for b in range(nblk)}
-    # causal work of a block: forward query block qb sees qb+1 key tiles, backward key block kb
-    # sees T/64 - 4kb query tiles; within a pair the dispatch order is non-increasing in work
-    work = (wm[:, 1] + 1) if kind == 0 else (T // 64 - 4 * wm[:, 1])
+    # causal work of a block: a query block qb (forward, dQ) sees qb+1 key blocks, a key block kb
+    # (dK/dV) sees T/64 - 2kb query tiles; within a pair the dispatch order is non-increasing in work
+    work = (wm[:, 1] + 1) if kind != 1 else (T // 64 - 2 * wm[:, 1])
     for p in range(npairs):
         w = work[wm[:, 0] == p]
         assert (np.diff(w) <= 0).all()
