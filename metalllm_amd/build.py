@@ -28,9 +28,10 @@ FLAGS = [
 ]
 
 
-# Per-source extra flags: the backward kernels' per-tile slot loops are fully unrolled (their
-# register arrays are indexed by the slot), which exceeds the default unroll size limit.
+# Per-source extra flags: the kernels' per-tile slot loops are fully unrolled (their register
+# arrays are indexed by the slot), which exceeds the default unroll size limit.
 EXTRA = {
+    "attn_fwd.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
     "attn_bwd.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
     "attn_bwd_dq.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
 }

@@ -59,10 +59,6 @@ __device__ __forceinline__ u32x2 lds_tr_b(uint32_t byte_addr) {
                                        (__attribute__((address_space(3))) i16x4*)(uintptr_t)byte_addr));
 }
 
-// Anchors: an empty asm that reads and rewrites a value pins its computation to this point of
-// the program (code motion cannot move the work into another slot).
-__device__ __forceinline__ void pin(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
-__device__ __forceinline__ void pin(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
 template <bool V>
 struct DiagTag {

@@ -60,10 +60,6 @@ __device__ __forceinline__ void g2lds16(const void* src, void* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
 }
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
-// Anchors: an empty asm that reads and rewrites a value pins its computation to this point of
-// the program (code motion cannot move the work into another slot).
-__device__ __forceinline__ void pin(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
-__device__ __forceinline__ void pin(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_u16*)p; }
 __device__ __forceinline__ u32x4 lds_b128_at(uint32_t byte_addr) {

@@ -83,6 +83,19 @@ __device__ __forceinline__ void round_pair(f32x16& v, int r) {
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) in one v_max3_f32 (fmaxf would first canonicalise operands that come from bit
+// operations, one extra instruction each).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Anchors: an empty asm that reads and rewrites a value pins its computation to this point of
+// the program (code motion cannot move the work into another slot of a fenced schedule).
+__device__ __forceinline__ void pin(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
+__device__ __forceinline__ void pin(uint32_t& a) { asm volatile("" : "+v"(a)); }
+
 // v_permlane32_swap(x, x) returns {lanes 0-31: own, 32-63: partner} and {lanes 0-31: partner,
 // 32-63: own}, partner = lane ^ 32. Combining the two with a commutative op gives every lane
 // op(own, partner), bit-identical in both halves.

@@ -54,14 +54,6 @@ struct FwdCfg {
   static constexpr int DT = D / 32;                         // 32-wide d tiles of the output
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Copies 64 lanes x 16 bytes from per-lane global addresses into 1 KB of LDS at `dst` (lane i
-// writes dst + 16 i).
-__device__ __forceinline__ void g2lds(const void* src, void* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
-}
-
 template <int D>
 struct FwdState {
   f32x16 O[D / 32];
@@ -69,58 +61,10 @@ struct FwdState {
   bool rescale;
 };
 
-// Softmax of one 64-key tile held as two S^T subtiles (lane = query): rounding points, mask,
-// running max with threshold, exponentials, row sum and packed P.
-template <int D, bool MASK>
-__device__ __forceinline__ void softmax_tile(const f32x16& S0, const f32x16& S1, FwdState<D>& st, uint32_t (&P)[16],
-                                             float scale, float c1, int key0, int q, int h) {
-  float x[32];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    x[r] = S0[r];
-    x[16 + r] = S1[r];
-  }
-#pragma unroll
-  for (int i = 0; i < 32; i += 2) {
-    round_pair(x[i], x[i + 1]);
-    if (D != 64) {
-      x[i] *= scale;
-      x[i + 1] *= scale;
-      round_pair(x[i], x[i + 1]);
-    }
-  }
-  if (MASK) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int r = i & 15;
-      const int key = key0 + 32 * (i >> 4) + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (key > q) x[i] = -INFINITY;
-    }
-  }
-  float mt = fmaxf(x[0], x[1]);
-#pragma unroll
-  for (int i = 2; i < 32; i += 2) mt = fmaxf(mt, fmaxf(x[i], x[i + 1]));
-  mt = max_halves(mt);
-  // threshold 8 in log2 units; true on the first tile (m_use = -inf). Branch-free, so that the
-  // scheduler can interleave the whole tile with the matrix-core work of the pipeline step.
-  const bool need = (mt - st.m_use) * c1 > 8.0f;
-  st.rescale = __any(need);
-  const float m_new = need ? mt : st.m_use;
-  st.alpha = exp2_hw((st.m_use - m_new) * c1);  // exactly 1 where m stays, 0 on the first tile
-  st.l_run *= st.alpha;
-  st.m_use = m_new;
-  const float mb = st.m_use * c1;
-  float ls = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i += 2) {
-    const float e0 = exp2_hw(fmaf(x[i], c1, -mb));
-    const float e1 = exp2_hw(fmaf(x[i + 1], c1, -mb));
-    ls += e0;
-    ls += e1;
-    P[i >> 1] = pack_bf16(e0, e1);
-  }
-  st.l_run += ls;
-}
+template <bool S_, bool PV_, bool SM_, bool DIAG_>
+struct StepFlags {
+  static constexpr bool S = S_, PV = PV_, SM = SM_, DIAG = DIAG_;
+};
 
 template <int D>
 __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
@@ -167,19 +111,22 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     const int s = 64 * (wave + 4 * j) + lane, row = s / C::VSLOTS, c = min(s % C::VSLOTS, D / 8 - 1);
     voff[j] = (uint32_t)(row * rs * 2 + c * 16);
   }
+  // The copies are untracked by the compiler (dma16): sync() waits for them before the barrier
+  // that precedes any read of the stage.
+  const uint32_t smem_a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
   auto load_k = [&](int kt, int stage) {
     const char* src = Kg + (size_t)kt * tile_bytes;
-    unsigned char* dst = smem + stage * C::STAGE;
+    const uint32_t dst = smem_a + stage * C::STAGE;
 #pragma unroll
     for (int j = 0; j < C::KPW; ++j)
-      if (wave + 4 * j < C::KSLOTS) g2lds(src + koff[j], dst + 1024 * (wave + 4 * j));
+      if (wave + 4 * j < C::KSLOTS) dma16(koff[j], src, dst + 1024 * (wave + 4 * j));
   };
   auto load_v = [&](int kt, int stage) {
     const char* src = Vg + (size_t)kt * tile_bytes;
-    unsigned char* dst = smem + stage * C::STAGE + C::KBYTES;
+    const uint32_t dst = smem_a + stage * C::STAGE + C::KBYTES;
 #pragma unroll
     for (int j = 0; j < C::VPW; ++j)
-      if (wave + 4 * j < C::VSLOTS) g2lds(src + voff[j], dst + 1024 * (wave + 4 * j));
+      if (wave + 4 * j < C::VSLOTS) dma16(voff[j], src, dst + 1024 * (wave + 4 * j));
   };
 
   // Per-lane LDS operand bases (element offsets inside a stage).
@@ -200,28 +147,6 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
       S1 = mfma(lds_read16(kb + 32 * C::KP + 16 * c), Qr[c], S1);
     }
   };
-  auto pv_tile = [&](int stage, const uint32_t (&P)[16], FwdState<D>& st) {
-    const uint16_t* vb = (const uint16_t*)(smem + stage * C::STAGE + C::KBYTES) + v_rd;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 Bp = {P[4 * c], P[4 * c + 1], P[4 * c + 2], P[4 * c + 3]};
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        const u32x2 lo = lds_tr(vb + 16 * c * C::VP + 32 * dt);
-        const u32x2 hi = lds_tr(vb + (16 * c + 8) * C::VP + 32 * dt);
-        st.O[dt] = mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, Bp, st.O[dt]);
-      }
-    }
-  };
-  auto apply_rescale = [&](FwdState<D>& st) {
-    if (st.rescale) {
-      asm volatile("" ::: "memory");  // keeps the rare rescale behind its branch
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) st.O[dt][r] *= st.alpha;
-    }
-  };
 
   FwdState<D> st;
 #pragma unroll
@@ -235,65 +160,222 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   const float su = (D == 64) ? 0.125f : 1.0f;
   const float c1 = su * kLog2e;
 
+  // O *= alpha before the P.V of a tile whose softmax moved the running max (rare)
+  auto apply_rescale = [&]() {
+    if (st.rescale) {
+      asm volatile("" ::: "memory");  // keeps the rare rescale behind its branch
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st.O[dt][r] *= st.alpha;
+    }
+  };
+
+  // One pipeline step of a wave, kt: S(kt+1) (if DO_S), O += P(kt-1).V(kt-1) (if DO_PV) and the
+  // softmax of tile kt (if DO_SM; masked if DIAG, the wave's diagonal tile), reading K(kt+1) and
+  // V(kt-1) from LDS stage `rd`. The matrix-core instructions run in a fixed order, one per slot
+  // (all P.V, then all S); each slot also issues the LDS operand reads of the
+  // instruction two slots ahead and a slice of the softmax, which does not depend on that
+  // slot's products. Softmax slots [0, AEND): rounding points, mask and the tile max of the raw
+  // products (two scores per pair); slot AEND: running max, factor and rescale flag; slots (AEND, NV):
+  // exponentials, row sum and packed P. Scheduling fences keep the order. Xc = S^T of tile kt
+  // (in), Xn = S^T of tile kt+1 (out), Pin = P of tile kt-1, Pout = P of tile kt.
+  auto wstep = [&](auto flags, int kt, int rd, const f32x16& Xc0, const f32x16& Xc1, f32x16& Xn0, f32x16& Xn1,
+                   const uint32_t(&Pin)[16], uint32_t(&Pout)[16]) __attribute__((always_inline)) {
+    using F = decltype(flags);
+    if (F::PV) apply_rescale();
+    const uint16_t* kb = (const uint16_t*)(smem + rd * C::STAGE) + k_rd;
+    const uint16_t* vb = (const uint16_t*)(smem + rd * C::STAGE + C::KBYTES) + v_rd;
+    constexpr int NSM = F::S ? 2 * C::KC : 0;  // S products
+    constexpr int NPV = F::PV ? 4 * C::DT : 0;  // P.V products
+    constexpr int NM = NSM + NPV;
+    // Softmax schedule, software-pipelined over score pairs (p = elements 2p, 2p+1) so that a
+    // slot carries independent chains: phase A (stages: A1 mask, running max, bf16(S); for
+    // D=128 also A2 scale, A3 bf16 again) of pair p in slot p/APS + stage; phase B (running max,
+    // factor, rescale flag) in slot BSLOT, right after the last A1; phase C (C1 exponent
+    // argument, C2 exp2, C3 row sum and packed P) of pair p in slot BSLOT + 1 + p/CPS + stage.
+    constexpr int APS = D == 64 ? 2 : 1;
+    constexpr int ANS = D == 64 ? 1 : 3;
+    constexpr int BSLOT = 16 / APS;
+    constexpr int CPS = D == 64 ? 4 : 2;
+    constexpr int LAST = BSLOT + 1 + 15 / CPS + 2;
+    constexpr int NV = NM > LAST + 1 ? NM : LAST + 1;  // slots
+    // product i: kind (0 = S, 1 = P.V) and index j within its kind. The P.V products come first,
+    // so that S(kt+1) starts accumulating once the scores of tile kt have been rounded and P(kt-1)
+    // has been consumed (the two live ranges do not overlap).
+    auto kind = [&](int i) -> int { return i < NPV ? 1 : 0; };
+    auto index = [&](int i) -> int { return i < NPV ? i : i - NPV; };
+    auto operand = [&](int i) -> u32x4 {
+      const int j = index(i);
+      if (kind(i)) {  // P.V product j: key chunk c, d tile dt
+        const int c = j / C::DT, dt = j % C::DT;
+        const u32x2 lo = lds_tr(vb + 16 * c * C::VP + 32 * dt);
+        const u32x2 hi = lds_tr(vb + (16 * c + 8) * C::VP + 32 * dt);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+      return lds_read16(kb + (j & 1) * 32 * C::KP + 16 * (j >> 1));  // S product j: half j&1, d step j>>1
+    };
+    constexpr int RING = 4;  // operand reads run RING-1 slots ahead of their product
+    u32x4 ring[RING];
+#pragma unroll
+    for (int i = 0; i < RING - 1; ++i)
+      if (i < NM) ring[i] = operand(i);
+    float mxa = -INFINITY, mxb = -INFINITY, ls0 = 0.0f, ls1 = 0.0f, mb = 0.0f;
+    uint32_t X[16], pk1[16];  // bf16 scores of tile kt, pairs (2p, 2p+1)
+    float u0[16], u1[16], t0[16], t1[16], e0[16], e1[16];
+    // key > q  <=>  off(e) > q - kt*64 - 4h; opaque, so that the compares are not rewritten
+    // against 32 loop-invariant bounds
+    int dq = q - kt * C::BN - 4 * h;
+    if (F::DIAG) asm volatile("" : "+v"(dq));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (i < NM) {
+        if (i + RING - 1 < NM) ring[(i + RING - 1) % RING] = operand(i + RING - 1);
+        const int j = index(i);
+        const u32x4& op = ring[i % RING];
+        if (kind(i)) {
+          const int c = j / C::DT, dt = j % C::DT;
+          st.O[dt] = mfma(op, u32x4{Pin[4 * c], Pin[4 * c + 1], Pin[4 * c + 2], Pin[4 * c + 3]}, st.O[dt]);
+        } else if (j & 1) {
+          Xn1 = mfma(op, Qr[j >> 1], (j >> 1) ? Xn1 : zero16());
+        } else {
+          Xn0 = mfma(op, Qr[j >> 1], (j >> 1) ? Xn0 : zero16());
+        }
+      }
+      if (F::SM) {
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+          const int sa = i - p / APS;  // phase A stage of pair p in this slot
+          if (sa == 0) {
+            const f32x16& Xs = p < 8 ? Xc0 : Xc1;
+            float a0 = Xs[(2 * p) & 15], a1 = Xs[(2 * p + 1) & 15];
+            if (F::DIAG) {  // key of element e = kt*64 + 4h + off(e), off(e) = 32(e/16) + 8((e%16)/4) + e%4
+              const int e = 2 * p, off = 32 * (e >> 4) + 8 * ((e & 15) >> 2) + (e & 3);
+              if (off > dq) a0 = -INFINITY;
+              if (off + 1 > dq) a1 = -INFINITY;
+            }
+            if (p & 1)
+              mxb = max3f(mxb, a0, a1);
+            else
+              mxa = max3f(mxa, a0, a1);
+            pk1[p] = pack_bf16(a0, a1);
+            pin(pk1[p]);
+            if (D == 64) X[p] = pk1[p];
+          } else if (D != 64 && sa == 1) {
+            u0[p] = bf_lo(pk1[p]) * a.scale;
+            u1[p] = bf_hi(pk1[p]) * a.scale;
+            pin(u0[p], u1[p]);
+          } else if (D != 64 && sa == 2) {
+            X[p] = pack_bf16(u0[p], u1[p]);
+            pin(X[p]);
+          }
+        }
+        if (i == BSLOT) {
+          // the rounding points are monotone, so the rounded raw max is the max of the rounded
+          // scores (exact reference point: the largest score's exponential is exactly 1)
+          float mt = bf_lo(pack_bf16(max_halves(fmaxf(mxa, mxb)), 0.0f));
+          if (D != 64) mt = bf_lo(pack_bf16(mt * a.scale, 0.0f));
+          // threshold 8 in log2 units; true on the first tile (m_use = -inf)
+          const bool need = (mt - st.m_use) * c1 > 8.0f;
+          st.rescale = __any(need);
+          const float m_new = need ? mt : st.m_use;
+          st.alpha = exp2_hw((st.m_use - m_new) * c1);  // exactly 1 where m stays, 0 on the first tile
+          st.l_run *= st.alpha;
+          st.m_use = m_new;
+          mb = st.m_use * c1;
+        }
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+          const int sc = i - (BSLOT + 1 + p / CPS);  // phase C stage of pair p in this slot
+          if (sc == 0) {
+            t0[p] = fmaf(bf_lo(X[p]), c1, -mb);
+            t1[p] = fmaf(bf_hi(X[p]), c1, -mb);
+            pin(t0[p], t1[p]);
+          } else if (sc == 1) {
+            e0[p] = exp2_hw(t0[p]);
+            e1[p] = exp2_hw(t1[p]);
+            pin(e0[p], e1[p]);
+          } else if (sc == 2) {
+            ls0 = p ? ls0 + e0[p] : e0[p];
+            ls1 = p ? ls1 + e1[p] : e1[p];
+            pin(ls0, ls1);  // keeps the sum in this slot (else the exponentials stay live to the end)
+            uint32_t pk = pack_bf16(e0[p], e1[p]);
+            pin(pk);
+            Pout[p] = pk;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (F::SM) st.l_run += ls0 + ls1;
+  };
+
   f32x16 Sc0 = zero16(), Sc1 = zero16(), Sn0 = zero16(), Sn1 = zero16();  // S^T: current tile, next tile
-  uint32_t Pc[16], Pp[16];     // P of the current tile, and of the previous one
+  uint32_t Pc[16], Pp[16];  // P of the current tile, and of the previous one
+#pragma unroll
+  for (int i = 0; i < 16; ++i) Pc[i] = Pp[i] = 0u;
 
   // ---- prologue: K(0) -> stage 0, K(1) -> stage 1; S(0) ----
   load_k(0, 0);
   if (n_tiles > 1) load_k(1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (my_tiles > 0) s_tile(0, Sc0, Sc1);
+  s_tile(0, Sc0, Sc1);
   __syncthreads();
 
-  // One pipeline step: loads K(kt+2), V(kt) -> stage kt&1; reads K(kt+1), V(kt-1) from the other.
-  auto step = [&](int kt, bool do_s, bool do_pv, bool do_sm, bool diag) {
-    if (kt + 2 < n_tiles) load_k(kt + 2, kt & 1);
-    load_v(kt, kt & 1);
-    const int rd = (kt + 1) & 1;
-    if (do_s) s_tile(rd, Sn0, Sn1);
-    if (do_pv) pv_tile(rd, Pp, st);
-    if (do_sm) {
-      if (diag)
-        softmax_tile<D, true>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
-      else
-        softmax_tile<D, false>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
-      apply_rescale(st);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Pp[i] = Pc[i];
-    Sc0 = Sn0;
-    Sc1 = Sn1;
+  // Step kt of the workgroup: every wave loads K(kt+2) and V(kt) into stage kt&1 (which steps
+  // up to kt-1 finished reading), runs the step, then all wait for the copies. All waves run
+  // the same steps (no per-wave branches): tiles from full_end on are the diagonal region and
+  // are masked per lane, and a tile entirely above a wave's rows adds exact zeros (P = 0, the
+  // running max and sum unchanged).
+  auto sync = [&]() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
-
-  // Tiles 0 .. full_end-1 are below every wave's diagonal (no mask), and every wave is active.
-  const int full_end = q0 / C::BN;
-  int kt = 0;
-  if (full_end >= 2) {
-    step(0, true, false, true, false);
-    for (kt = 1; kt + 1 < full_end; ++kt) {
-      // steady state: S(kt+1) full, P.V(kt-1), softmax(kt) full; kt+2 <= full_end < n_tiles
-      load_k(kt + 2, kt & 1);
-      load_v(kt, kt & 1);
-      const int rd = (kt + 1) & 1;
-      s_tile(rd, Sn0, Sn1);
-      pv_tile(rd, Pp, st);
-      softmax_tile<D, false>(Sc0, Sc1, st, Pc, a.scale, c1, kt * C::BN, q, h);
-      apply_rescale(st);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) Pp[i] = Pc[i];
+  // a step with the buffers in their canonical places (Sc = S(kt), Pp = P(kt-1)); the outputs
+  // are moved back into place after it
+  auto run = [&](auto flags, int kt) __attribute__((always_inline)) {
+    using F = decltype(flags);
+    if (kt + 2 < n_tiles) load_k(kt + 2, kt & 1);
+    if (kt < n_tiles) load_v(kt, kt & 1);
+    wstep(flags, kt, (kt + 1) & 1, Sc0, Sc1, Sn0, Sn1, Pp, Pc);
+    if (F::S) {
       Sc0 = Sn0;
       Sc1 = Sn1;
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
     }
+    if (F::SM) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Pp[i] = Pc[i];
+    }
+    sync();
+  };
+
+  const int full_end = q0 / C::BN;  // tiles 0 .. full_end-1 are below every row of the workgroup
+  if (n_tiles == 1)
+    run(StepFlags<false, false, true, true>(), 0);
+  else if (full_end == 0)
+    run(StepFlags<true, false, true, true>(), 0);
+  else
+    run(StepFlags<true, false, true, false>(), 0);
+  int kt = 1;
+  // steady steps kt = 1 .. full_end-1, two per iteration with the S and P buffers swapping
+  // roles (an odd count starts with one step that moves its outputs back)
+  if (full_end - kt >= 1 && ((full_end - kt) & 1)) run(StepFlags<true, true, true, false>(), kt++);
+  for (; kt + 1 < full_end; kt += 2) {
+    if (kt + 2 < n_tiles) load_k(kt + 2, kt & 1);
+    load_v(kt, kt & 1);
+    wstep(StepFlags<true, true, true, false>(), kt, (kt + 1) & 1, Sc0, Sc1, Sn0, Sn1, Pp, Pc);
+    sync();
+    if (kt + 3 < n_tiles) load_k(kt + 3, (kt + 1) & 1);
+    load_v(kt + 1, (kt + 1) & 1);
+    wstep(StepFlags<true, true, true, false>(), kt + 1, kt & 1, Sn0, Sn1, Sc0, Sc1, Pc, Pp);
+    sync();
   }
-  for (; kt < n_tiles; ++kt)
-    step(kt, kt + 1 < my_tiles, kt >= 1 && kt - 1 < my_tiles, kt < my_tiles, kt == my_tiles - 1);
-  // last P.V of waves whose diagonal is the workgroup's last tile
-  if (my_tiles == n_tiles && my_tiles > 0) pv_tile((n_tiles - 1) & 1, Pp, st);
+  // diagonal region (at most two tiles)
+  if (kt + 1 < n_tiles) run(StepFlags<true, true, true, true>(), kt++);
+  if (kt < n_tiles) run(StepFlags<false, true, true, true>(), kt++);
+  // P.V of the last tile
+  wstep(StepFlags<false, true, false, false>(), n_tiles, (n_tiles - 1) & 1, Sc0, Sc1, Sn0, Sn1, Pp, Pc);
 
   if (!wave_active) return;
   // ---- epilogue: out = bf16(O * (1/l)), lse = m + log(l) ----
