@@ -27,7 +27,8 @@
 // keys 32-63, then the dQ products; p and dS of the first 32 keys are computed while the
 // second half's products run, and dS of the second half while the first dQ products run.
 // Scheduling fences keep that order. K and V tiles go global -> LDS by
-// global_load_lds_dwordx4 (no registers), two stages: tile j+1 is copied while tile j is used.
+// global_load_lds_dwordx4 (no registers, untracked by the compiler), two stages: tile j+1 is
+// copied while tile j is used.
 //
 // Matrix-core passes: S and dP sum d in passes of 8 consecutive values; dQ sums keys in passes
 // {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}.
@@ -49,16 +50,32 @@ struct DqCfg {
   static constexpr int KC = D / 16;                      // 16-deep steps over d
   static constexpr int DT = D / 32;                      // 32-wide d tiles of dQ
   static constexpr int NM = 4 * KC + 4 * DT;             // matrix-core instructions per tile
-  static constexpr int PPS = 8 / KC;                     // score pairs of vector work per slot (1 or 2)
   static constexpr int DQP = D + 4;                      // fp32 pitch of the dQ transpose buffer
+  // Vector-work schedule: score pair p of half t enters its four stages in slot enter(t, p) and
+  // packs dS in slot enter + 3; pairs per slot PPS (two at D=64, where there are fewer products).
+  static constexpr int PPS = D == 64 ? 2 : 1;
+  static constexpr int enter(int t, int p) { return (t ? 4 * KC : 2 * KC) + p / PPS; }
+  // slot of dQ product k (key chunk c = k / DT, d tile k % DT): in order, after the slot that
+  // packs the last dS pair of chunk c (pairs 4(c%2) .. +3 of half c/2)
+  static constexpr int dq_slot(int k) {
+    int slot = 4 * KC - 1;
+    for (int j = 0; j <= k; ++j) {
+      const int c = j / DT, ready = enter(c / 2, 4 * (c % 2) + 3) + 3;
+      slot = (slot + 1 > ready + 1) ? slot + 1 : ready + 1;
+    }
+    return slot;
+  }
+  static constexpr int NV = dq_slot(4 * DT - 1) + 1;  // slots per tile
+  // matrix-core product of slot i (S/dP: i < 4KC; dQ: 4KC + k), or -1
+  static constexpr int product_at(int i) {
+    if (i < 4 * KC) return i;
+    for (int k = 0; k < 4 * DT; ++k)
+      if (dq_slot(k) == i) return 4 * KC + k;
+    return -1;
+  }
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) uint16_t lds_u16;
-
-__device__ __forceinline__ void g2lds16(const void* src, void* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-}
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_u16*)p; }
@@ -122,15 +139,17 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
     const int sl_ = 64 * (wave + 4 * j) + lane, row = sl_ / C::SLOTS, c = min(sl_ % C::SLOTS, D / 8 - 1);
     off[j] = (uint32_t)(row * rs * 2 + c * 16);
   }
+  // untracked copies (dma16): the s_waitcnt before each barrier covers them, and the LDS reads
+  // of the current tile do not wait for the next tile's copy
   auto issue_tile = [&](int kt) {
     const char* ks = Kg + (size_t)kt * tile_bytes;
     const char* vs = Vg + (size_t)kt * tile_bytes;
-    unsigned char* dst = smem + (kt & 1) * C::STAGE;
+    const uint32_t dst = lds_addr(smem + (kt & 1) * C::STAGE);
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j)
       if (wave + 4 * j < C::SLOTS) {
-        g2lds16(ks + off[j], dst + 1024 * (wave + 4 * j));
-        g2lds16(vs + off[j], dst + C::TBYTES + 1024 * (wave + 4 * j));
+        dma16(off[j], ks, dst + 1024 * (wave + 4 * j));
+        dma16(off[j], vs, dst + C::TBYTES + 1024 * (wave + 4 * j));
       }
   };
 
@@ -161,70 +180,99 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   for (int i = 0; i < C::DT; ++i) dQa[i] = zero16();
   uint32_t dS[16];
 
-  // One key tile (MASK: this wave's diagonal tile). x = S^T (then p in place), y = dP^T, per
-  // 32-key half; pair r of half t is scores (r, r+1) of register block t.
+  // One key tile (MASK: this wave's diagonal tile). x = S^T, y = dP^T per 32-key half t; pair p
+  // of half t is scores (2p, 2p+1) of register block t. Matrix-core slots: [0, 2KC) S and dP of
+  // half 0 alternating (d step c = i/2), [2KC, 4KC) the same for half 1, [4KC, NM) dQ ordered by
+  // key chunk c (keys 16c..16c+15) then d tile. The vector work of a pair runs in four pipelined
+  // stages (1: bf16(S) and the exponent argument; 2: exp2, bf16(dP); 3: dP - D and p*(dP - D);
+  // 4: *scale and packed dS), pair p of half t entering in slot DqCfg::enter(t, p); a dQ product
+  // of chunk c waits (DqCfg::dq_slot) until the dS pairs of keys 16c.. are packed, which at
+  // D=64 inserts slots without a product.
   auto tile = [&](int kt, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const uint32_t kb = lds_addr(smem + (kt & 1) * C::STAGE), vb = kb + C::TBYTES;
     const int key0 = kt * C::BN;
     f32x16 x0 = zero16(), x1 = zero16(), y0 = zero16(), y1 = zero16();
-    // p for score pair (r, r+1) of half t: s = bf16(S), p = exp2(s*scale*log2e - lse*log2e),
-    // 0 above the diagonal
-    auto p_pair = [&](f32x16& x, int t, int r) {
-      round_pair(x, r);
-      float p0 = exp2_hw(fmaf(x[r], sl, -lse2));
-      float p1 = exp2_hw(fmaf(x[r + 1], sl, -lse2));
-      if (MASK) {
-        const int k0 = key0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (k0 > q) p0 = 0.0f;
-        if (k0 + 1 > q) p1 = 0.0f;
+    // operand reads run AHEAD(i) products ahead: five during the first S/dP half (no vector work
+    // there to cover the LDS latency), two afterwards
+    constexpr int RING = 6;
+    auto ahead = [](int i) { return i < 2 * C::KC ? 5 : 2; };
+    u32x4 ring[RING];
+    auto op_of = [&](int i) -> u32x4 {
+      if (i < 4 * C::KC) {  // S / dP: half t, d step c
+        const int t = i / (2 * C::KC), isdp = i & 1, c = (i % (2 * C::KC)) >> 1;
+        return lds_b128_at((isdp ? vb : kb) + row_rd + 2 * (32 * t * C::P + 16 * c));
       }
-      pin(p0, p1);
-      x[r] = p0;
-      x[r + 1] = p1;
+      const int k = i - 4 * C::KC, dt = k % C::DT, c = k / C::DT;
+      const u32x2 lo = lds_tr_at(kb + tr_rd + 2 * (16 * c * C::P + 32 * dt));
+      const u32x2 hi = lds_tr_at(kb + tr_rd + 2 * ((16 * c + 8) * C::P + 32 * dt));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
-    // dS = bf16(p * (bf16(dP) - D) * scale) for score pair (r, r+1) of half t
-    auto ds_pair = [&](const f32x16& x, f32x16& y, int t, int r) {
-      round_pair(y, r);
-      const float d0 = (x[r] * (y[r] - dq)) * scale;
-      const float d1 = (x[r + 1] * (y[r + 1] - dq)) * scale;
-      uint32_t pk = pack_bf16(d0, d1);
-      pin(pk);
-      dS[8 * t + (r >> 1)] = pk;
-    };
-    u32x4 ring[2];  // operand of slot i is read during slot i-1
-    ring[0] = operand(0, kb, vb);
 #pragma unroll
-    for (int i = 0; i < C::NM; ++i) {
-      if (i + 1 < C::NM) ring[(i + 1) % 2] = operand(i + 1, kb, vb);
-      const u32x4& op = ring[i % 2];
-      const int seg = i / C::KC;  // 0: S0, 1: dP0, 2: S1, 3: dP1, 4..: dQ
-      if (seg == 0)
-        x0 = mfma(op, Qr[i % C::KC], x0);
-      else if (seg == 1)
-        y0 = mfma(op, Gr[i % C::KC], y0);
-      else if (seg == 2)
-        x1 = mfma(op, Qr[i % C::KC], x1);
-      else if (seg == 3)
-        y1 = mfma(op, Gr[i % C::KC], y1);
-      else {
+    for (int i = 0; i <= ahead(0); ++i) ring[i] = op_of(i);
+    uint32_t sb[16], db[16];
+    float ta[16], tb[16], pa[16], pb[16], ya[16], yb[16];
+    // vector stage st of pair p of half t (pair index u = 8t + p)
+    auto stage = [&](int t, int p, int st) {
+      f32x16& x = t ? x1 : x0;
+      f32x16& y = t ? y1 : y0;
+      const int u = 8 * t + p, r = 2 * p;
+      if (st == 0) {  // s = bf16(S); exponent argument s*scale*log2e - lse*log2e
+        sb[u] = pack_bf16(x[r], x[r + 1]);
+        ta[u] = fmaf(bf_lo(sb[u]), sl, -lse2);
+        tb[u] = fmaf(bf_hi(sb[u]), sl, -lse2);
+        pin(ta[u], tb[u]);
+      } else if (st == 1) {  // p = exp2(.), 0 above the diagonal; bf16(dP)
+        float p0 = exp2_hw(ta[u]), p1 = exp2_hw(tb[u]);
+        if (MASK) {
+          const int k0 = key0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (k0 > q) p0 = 0.0f;
+          if (k0 + 1 > q) p1 = 0.0f;
+        }
+        pa[u] = p0;
+        pb[u] = p1;
+        db[u] = pack_bf16(y[r], y[r + 1]);
+        pin(pa[u], pb[u]);
+        pin(db[u]);
+      } else if (st == 2) {  // p * (dP - D)
+        ya[u] = pa[u] * (bf_lo(db[u]) - dq);
+        yb[u] = pb[u] * (bf_hi(db[u]) - dq);
+        pin(ya[u], yb[u]);
+      } else {  // dS = bf16(p * (dP - D) * scale)
+        uint32_t pk = pack_bf16(ya[u] * scale, yb[u] * scale);
+        pin(pk);
+        dS[u] = pk;
+      }
+    };
+#pragma unroll
+    for (int slot = 0; slot < C::NV; ++slot) {
+      const int i = C::product_at(slot);
+      if (i >= 0) {
+#pragma unroll
+      for (int k = (i ? i - 1 + ahead(i - 1) : ahead(0)) + 1; k <= i + ahead(i) && k < C::NM; ++k)
+        ring[k % RING] = op_of(k);
+      const u32x4& op = ring[i % RING];
+      if (i < 4 * C::KC) {
+        const int t = i / (2 * C::KC), c = (i % (2 * C::KC)) >> 1;
+        if (i & 1) {
+          if (t) y1 = mfma(op, Gr[c], y1);
+          else y0 = mfma(op, Gr[c], y0);
+        } else {
+          if (t) x1 = mfma(op, Qr[c], x1);
+          else x0 = mfma(op, Qr[c], x0);
+        }
+      } else {
         const int k = i - 4 * C::KC, dt = k % C::DT, c = k / C::DT;
         dQa[dt] = mfma(op, u32x4{dS[4 * c], dS[4 * c + 1], dS[4 * c + 2], dS[4 * c + 3]}, dQa[dt]);
       }
-      // vector work of this slot: seg 1: p of half 0; seg 2: dS of half 0; seg 3: p of half 1;
-      // first dQ segment: dS of half 1 (8 pairs each, PPS per slot)
-#pragma unroll
-      for (int u = 0; u < C::PPS; ++u) {
-        const int r = 2 * ((i % C::KC) * C::PPS + u);
-        if (seg == 1)
-          p_pair(x0, 0, r);
-        else if (seg == 2)
-          ds_pair(x0, y0, 0, r);
-        else if (seg == 3)
-          p_pair(x1, 1, r);
-        else if (seg == 4)
-          ds_pair(x1, y1, 1, r);
       }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const int st = slot - C::enter(t, p);
+          if (st >= 0 && st < 4) stage(t, p, st);
+        }
       fence();
     }
   };
@@ -233,7 +281,18 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   issue_tile(0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int j = 0; j < n_tiles; ++j) {
+  // Tiles below every row of the workgroup run on every wave with one code path (inactive waves
+  // of a partial last block compute on zero rows and never store), so the accumulators keep
+  // their registers across iterations; the diagonal region (at most two tiles) branches per wave.
+  const int full_end = min(q0 / C::BN, n_tiles);
+  int j = 0;
+  for (; j < full_end; ++j) {
+    if (j + 1 < n_tiles) issue_tile(j + 1);
+    tile(j, BoolTag<false>());
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (; j < n_tiles; ++j) {
     if (j + 1 < n_tiles) issue_tile(j + 1);
     if (j + 1 < my_tiles)
       tile(j, BoolTag<false>());
