@@ -8,9 +8,11 @@ synthetic bf16 inputs already resident in HBM (the reference's per-layer sequenc
 549-551, 639-665). Prints ONE JSON line. FLOPs use the causal FlashAttention convention (half of
 dense): fwd 2*B*H*T^2*D, bwd 5*B*H*T^2*D, step 7*B*H*T^2*D.
 
-The roofline object describes the dominant kernel (flashAttentionBackward): its algorithmic FLOPs
-per launch over its average launch time measured with HIP events on the launch stream, against
-MI355X dense bf16 matrix peak. cpu_baseline times the CPU oracle (the scalar C++ transcription
+The roofline object describes the dominant kernel, the dK/dV kernel of flashAttentionBackward
+(mla::bwd_kernel; flashAttentionBackward launches it and then the dQ kernel, and the bench launches
+the two through metalllmAttnBackwardPart so that each has its own events): its algorithmic FLOPs
+per launch (4 causal products: S, dP, dV, dK) over its average launch time measured with HIP events
+on the launch stream, against MI355X dense bf16 matrix peak. cpu_baseline times the CPU oracle (the scalar C++ transcription
 of the reference math, oracle/attn_oracle.cpp) on a bounded sample of the same workload on this
 host's cores.
 """
@@ -42,8 +44,8 @@ def flops(B, H, T, D):
 
 
 def traffic_from_profiles(cfg_id):
-    """HBM bytes per backward launch measured by rocprofv3 --pmc, if a summary was committed."""
-    path = os.path.join(ROOT, "profiles", f"bwd_traffic_config{cfg_id}.json")
+    """HBM bytes per dK/dV-kernel launch measured by rocprofv3 --pmc, if a summary was committed."""
+    path = os.path.join(ROOT, "profiles", f"bwd_dkdv_traffic_config{cfg_id}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -117,6 +119,8 @@ def main():
     stream = torch.cuda.current_stream()
     p = M.AttentionParams.of(B, T, H, D)
 
+    # flashAttentionBackward == part 0 (dK/dV kernel) then part 1 (dQ kernel) on the same stream;
+    # the bench launches the parts itself so that each kernel is timed by its own events
     def step(ev=None):
         dQ.zero_()
         if ev is not None:
@@ -127,15 +131,18 @@ def main():
         M.computeD(dO, out, Dv, stream, p)
         if ev is not None:
             ev[2].record(stream)
-        M.flashAttentionBackward(dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
+        M.backward_part(0, dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
         if ev is not None:
             ev[3].record(stream)
+        M.backward_part(1, dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
+        if ev is not None:
+            ev[4].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -151,16 +158,17 @@ def main():
         torch.cuda.synchronize()
 
     # per-kernel times from the events (the dQ zeroing is in the step, outside the kernel intervals)
-    fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
-    cd_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
-    bwd_ms = sorted(e[2].elapsed_time(e[3]) for e in events)
+    span = lambda a, b: sorted(e[a].elapsed_time(e[b]) for e in events)
+    fwd_ms, cd_ms, kv_ms, dq_ms, bwd_ms = span(0, 1), span(1, 2), span(2, 3), span(3, 4), span(2, 4)
     avg = lambda xs: sum(xs) / len(xs)
     med = lambda xs: xs[len(xs) // 2]
     ff, fb = flops(B, H, T, D)
+    unit = B * H * T * T * D  # one causal T x T x D product over all (b, h)
     ms_per_step = wall * 1e3 / args.steps
     value = (ff + fb) / (ms_per_step * 1e-3) / 1e12
-    bwd_avg = avg(bwd_ms)
-    achieved = fb / (bwd_avg * 1e-3) / 1e12
+    # dominant kernel: the dK/dV kernel (4 products: S, dP, dV = P^T dO, dK = dS^T Q)
+    kv_avg = avg(kv_ms)
+    achieved = 4.0 * unit / (kv_avg * 1e-3) / 1e12
 
     bthd = B * T * H * D
     result = {
@@ -181,20 +189,22 @@ def main():
         "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "phases": {
             "fwd_ms_median": round(med(fwd_ms), 4), "computeD_ms_median": round(med(cd_ms), 4),
-            "bwd_ms_median": round(med(bwd_ms), 4),
+            "bwd_ms_median": round(med(bwd_ms), 4), "bwd_dkdv_ms_median": round(med(kv_ms), 4),
+            "bwd_dq_ms_median": round(med(dq_ms), 4),
             "fwd_tflops": round(ff / (med(fwd_ms) * 1e-3) / 1e12, 2),
             "bwd_tflops": round(fb / (med(bwd_ms) * 1e-3) / 1e12, 2),
             "computeD_gbs": round((4 * bthd + 4 * B * H * T) / (med(cd_ms) * 1e-3) / 1e9, 1),
         },
         "roofline": {
-            "kernel": "flashAttentionBackward",
+            "kernel": "flashAttentionBackward dK/dV kernel (mla::bwd_kernel)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic_from_profiles(args.config),
-            "algorithmic_bytes": 16 * bthd + 8 * B * H * T,
+            "algorithmic_bytes": 12 * bthd + 8 * B * H * T,
+            "avg_ms": round(kv_avg, 4),
         },
     }
     if not args.no_cpu_baseline:

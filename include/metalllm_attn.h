@@ -74,6 +74,15 @@ int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, c
                            const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                            const AttentionParams* p, metalllm_stream_t stream);
 
+/* Bench hook (no counterpart in the reference): launches one of the two kernels that
+ * flashAttentionBackward runs, in this order, on `stream`: part 0 = dK/dV (key-block owners),
+ * part 1 = dQ (query-block owners). flashAttentionBackward(args) is exactly part 0 followed by
+ * part 1, so timing the parts separately measures the same work. Same arguments, validation and
+ * return codes as flashAttentionBackward; part outside {0, 1} returns METALLLM_ATTN_E_LAYOUT. */
+int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                             const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                             const AttentionParams* p, metalllm_stream_t stream);
+
 /* Static description of an error code (no counterpart in the reference, which has no error
  * path per kernel; model.h:333-336,361-365 only print). */
 const char* metalllmAttnErrorString(int code);

@@ -3,8 +3,8 @@
 The product is libmetalllm_attn.so (C ABI in include/metalllm_attn.h); this package builds it
 (`metalllm_amd.build`) and binds it (`metalllm_amd.attention`).
 """
-from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, computeD,
-                        flashAttentionBackward, flashAttentionForward, library, work_map)
+from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, backward_part,
+                        computeD, flashAttentionBackward, flashAttentionForward, library, work_map)
 
-__all__ = ["AttentionError", "AttentionParams", "attention_backward", "attention_forward", "computeD",
-           "flashAttentionBackward", "flashAttentionForward", "library", "work_map"]
+__all__ = ["AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
+           "computeD", "flashAttentionBackward", "flashAttentionForward", "library", "work_map"]

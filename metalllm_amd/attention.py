@@ -21,8 +21,8 @@ OK = 0
 ERRORS = {
     -1: "E_NULL", -2: "E_SEQLEN", -3: "E_HEADDIM", -4: "E_LAYOUT", -5: "E_SIZE", -6: "E_ALIGN", -7: "E_LAUNCH",
 }
-EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnErrorString",
-            "metalllmAttnWorkMap")
+EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
+            "metalllmAttnErrorString", "metalllmAttnWorkMap")
 
 
 class AttentionParams(ctypes.Structure):
@@ -55,7 +55,8 @@ def _lib():
         L.flashAttentionForward.argtypes = [vp, vp, vp, vp, vp, pp, vp]
         L.computeD.argtypes = [vp, vp, vp, pp, vp]
         L.flashAttentionBackward.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, pp, vp]
-        for f in (L.flashAttentionForward, L.computeD, L.flashAttentionBackward):
+        L.metalllmAttnBackwardPart.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, pp, vp]
+        for f in (L.flashAttentionForward, L.computeD, L.flashAttentionBackward, L.metalllmAttnBackwardPart):
             f.restype = ctypes.c_int
         L.metalllmAttnErrorString.argtypes = [ctypes.c_int]
         L.metalllmAttnErrorString.restype = ctypes.c_char_p
@@ -115,6 +116,15 @@ def flashAttentionBackward(dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: A
     p = params or _shape(q)
     _check(_lib().flashAttentionBackward(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ), _ptr(dK),
                                          _ptr(dV), ctypes.byref(p), _stream(stream)), "flashAttentionBackward")
+
+
+def backward_part(part: int, dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None):
+    """One of the two kernels of flashAttentionBackward (0: dK/dV, 1: dQ); the bench times them
+    separately. Running part 0 then part 1 is flashAttentionBackward."""
+    p = params or _shape(q)
+    _check(_lib().metalllmAttnBackwardPart(part, _ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
+                                           _ptr(dK), _ptr(dV), ctypes.byref(p), _stream(stream)),
+           "metalllmAttnBackwardPart")
 
 
 def attention_forward(q, k, v, stream=None):

@@ -46,20 +46,29 @@ int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionPar
                                                                                 : METALLLM_ATTN_E_LAUNCH;
 }
 
-int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
-                           const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
-                           const AttentionParams* p, metalllm_stream_t stream) {
+int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                             const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                             const AttentionParams* p, metalllm_stream_t stream) {
   const int rc = validate(p);
   if (rc) return rc;
+  if (part != 0 && part != 1) return METALLLM_ATTN_E_LAYOUT;
   if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
   if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
     return METALLLM_ATTN_E_ALIGN;
   mla::BwdArgs a{dZ, d, l, q, k, v, dQ, dK, dV, (int)p->M, (int)p->NH, (int)p->B, head_scale(p->D)};
-  // dK/dV by the key owners, then dQ by the query owners (both on `stream`, in order)
-  if (mla::launch_backward(a, (int)p->D, (hipStream_t)stream) != hipSuccess) return METALLLM_ATTN_E_LAUNCH;
-  return mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
-                                                                                  : METALLLM_ATTN_E_LAUNCH;
+  const hipError_t e = part == 0 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
+                                 : mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream);
+  return e == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
+}
+
+int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                           const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                           const AttentionParams* p, metalllm_stream_t stream) {
+  // dK/dV by the key-block owners, then dQ by the query-block owners (both on `stream`, in order)
+  const int rc = metalllmAttnBackwardPart(0, dZ, d, l, q, k, v, dQ, dK, dV, p, stream);
+  if (rc) return rc;
+  return metalllmAttnBackwardPart(1, dZ, d, l, q, k, v, dQ, dK, dV, p, stream);
 }
 
 const char* metalllmAttnErrorString(int code) {

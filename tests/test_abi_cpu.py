@@ -43,6 +43,9 @@ def test_invalid_shapes_rejected_without_device(change, code):
     assert lib.flashAttentionForward(fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
     assert lib.computeD(fake, fake, fake, ctypes.byref(p), None) == code
     assert lib.flashAttentionBackward(fake, fake, fake, fake, fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
+    for part in (0, 1):
+        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+                                            ctypes.byref(p), None) == code
 
 
 def test_null_and_alignment_rejected():
@@ -56,6 +59,15 @@ def test_null_and_alignment_rejected():
     bad = ctypes.c_void_p((1 << 20) + 2)
     assert lib.flashAttentionForward(ok, ok, bad, ok, ok, ctypes.byref(p), None) == -6
     assert lib.computeD(ok, ok, bad, ctypes.byref(p), None) == -6
+
+
+def test_backward_part_rejects_unknown_part():
+    lib = M.library()
+    p = AttentionParams(256, 384, 64, 6, 1)
+    fake = ctypes.c_void_p(16)
+    for part in (-1, 2, 7):
+        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+                                            ctypes.byref(p), None) == -4
 
 
 def test_error_strings():

@@ -160,3 +160,28 @@ def test_backward_overwrites_dk_dv_and_accumulates_dq(gpu):
     M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
     assert torch.equal(dK, dK2) and torch.equal(dV, dV2)
     assert (dQ - 2 * dQ2).abs().max().item() <= 1e-5 * dQ2.abs().max().item()
+
+
+def test_backward_parts_equal_flash_attention_backward(gpu):
+    """The bench hook: part 0 (dK/dV kernel) then part 1 (dQ kernel) is flashAttentionBackward, bit
+    for bit (one fp32 atomic per dQ element into a zeroed buffer, so the order does not matter)."""
+    import torch
+    import metalllm_amd as M
+    q, k, v, g = make_inputs(2, 512, 3, 128, 41)
+    tq, tk, tv, tg = (to_gpu(x, gpu) for x in (q, k, v, g))
+    out, lse = M.attention_forward(tq, tk, tv)
+    Dv = torch.empty((2, 3, 512), dtype=torch.float32, device=gpu)
+    M.computeD(tg, out, Dv)
+    res = []
+    for split in (False, True):
+        dQ = torch.zeros((2, 512, 3, 128), dtype=torch.float32, device=gpu)
+        dK = torch.empty_like(tq)
+        dV = torch.empty_like(tq)
+        if split:
+            M.backward_part(0, tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+            M.backward_part(1, tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+        else:
+            M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+        res.append((dQ, dK, dV))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
