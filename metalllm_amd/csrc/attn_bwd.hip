@@ -189,8 +189,13 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     constexpr int NS = 4 * C::KC + 8 * C::DT;
     constexpr int PPS = 8 / C::KC;  // score pairs of vector work per S/dP slot
-    const uint32_t qbase_a = lds_addr_b(smem + stage * C::STAGE), gbase_a = qbase_a + C::TBYTES;
-    const uint32_t stat_a = qbase_a + C::STAT + st_rd;
+    // per-lane LDS bases of this stage, computed once and anchored so that every operand address
+    // below is base + constant (the constant goes into the instruction's offset field)
+    const uint32_t qbase_a = lds_addr_b(smem + stage * C::STAGE);
+    uint32_t row_a = qbase_a + row_rd, tr_a = qbase_a + tr_rd, stat_a = qbase_a + C::STAT + st_rd;
+    pin(row_a);
+    pin(tr_a);
+    pin(stat_a);
     const int qrow = qb * C::BM + 4 * h - key;  // q - key = qrow + 32t + 8g + i
     f32x16 x0 = zero16(), x1 = zero16(), y0 = zero16(), y1 = zero16();
     uint32_t Pp[16], dS[16];  // packed bf16: index 8t + r/2
@@ -198,10 +203,10 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
     auto operand = [&](int i) -> u32x4 {
       if (i < 4 * C::KC) {
         const int seg = i / C::KC, t = seg >> 1, c = i % C::KC;
-        return lds_b128_b(((seg & 1) ? gbase_a : qbase_a) + row_rd + 2 * (32 * t * C::P + 16 * c));
+        return lds_b128_b(row_a + ((seg & 1) ? C::TBYTES : 0) + 2 * (32 * t * C::P + 16 * c));
       }
       const int k = i - 4 * C::KC, n = k / 4, j = k % 4, dt = n % C::DT;
-      const uint32_t src = (n >= C::DT ? qbase_a : gbase_a) + tr_rd + 2 * (16 * j * C::P + 32 * dt);
+      const uint32_t src = tr_a + (n >= C::DT ? 0 : C::TBYTES) + 2 * (16 * j * C::P + 32 * dt);
       const u32x2 lo = lds_tr_b(src), hi = lds_tr_b(src + 2 * 8 * C::P);
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
@@ -260,17 +265,22 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
       dS[8 * t + u] = pk;
     };
 
-    u32x4 ring[2];
+    // operand reads run ahead(i) products ahead: four during the first S segment (almost no
+    // vector work there to cover the LDS latency), one afterwards; statistics one slot ahead
+    constexpr int RING = 5;
+    auto ahead = [](int i) { return i < C::KC ? 4 : 1; };
+    u32x4 ring[RING];
     f32x4 sring[2];
-    ring[0] = operand(0);
+#pragma unroll
+    for (int k = 0; k <= ahead(0); ++k) ring[k] = operand(k);
     sring[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      if (i + 1 < NS) {
-        ring[(i + 1) % 2] = operand(i + 1);
-        if (work(i + 1).kind) sring[(i + 1) % 2] = stats(i + 1);
-      }
-      const u32x4& op = ring[i % 2];
+#pragma unroll
+      for (int k = (i ? i - 1 + ahead(i - 1) : ahead(0)) + 1; k <= i + ahead(i) && k < NS; ++k)
+        ring[k % RING] = operand(k);
+      if (i + 1 < NS && work(i + 1).kind) sring[(i + 1) % 2] = stats(i + 1);
+      const u32x4& op = ring[i % RING];
       if (i < 4 * C::KC) {
         const int seg = i / C::KC, c = i % C::KC;
         if (seg == 0) x0 = mfma(op, Kr[c], x0);
