@@ -79,12 +79,88 @@ def cpu_baseline(B, H, T, D, qk_scale, threads):
     }
 
 
+def bench_sublayer(args):
+    """one pre-LN block's attention sublayer, fwd + bwd, X bf16 [8, 2048, 768]
+    ~N(0,1), Wq/Wk/Wv/Wproj bf16 [768, 768] ~N(0, 0.02), dOut ~N(0,1), H=12 (D=64). One step = the
+    gradient zeroing of model.h:549-555, then forward computeQKV -> flashAttentionForward ->
+    projForward and backward projBackwarddW/dX -> computeD -> flashAttentionBackward ->
+    computeGradDx/Dw (model.h:446-482, 621-690). Reports ms per step and the attention share."""
+    import torch
+    import metalllm_amd as M
+    from metalllm_amd import sublayer as S
+    B, T, C, H = 8, 2048, 768, 12
+    D = C // H
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    rn = lambda shape, sc=1.0: (torch.randn(shape, generator=gen, device=dev) * sc).to(torch.bfloat16)
+    X = rn((B, T, C))
+    Ws = [rn((C, C), 0.02) for _ in range(4)]
+    dOut = rn((B, T, C))
+    sub = S.Sublayer(X, *Ws, H=H)
+    stream = torch.cuda.current_stream()
+    names = ["zero", "qkv", "attn_fwd", "proj_fwd", "proj_bwd", "attn_bwd", "grad_dx_dw"]
+
+    def step(ev=None):
+        rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
+        rec(0)
+        sub.zero_grads()
+        rec(1)
+        S.computeQKV(sub.X, sub.q, sub.k, sub.v, sub.Wq, sub.Wk, sub.Wv, sub.p, stream)
+        rec(2)
+        M.flashAttentionForward(sub.q, sub.k, sub.v, sub.o, sub.lse, stream, sub.p)
+        rec(3)
+        S.projForward(sub.o, sub.Wp, sub.out, sub.p, stream)
+        rec(4)
+        marks = {"proj": 5, "attention": 6, "grads": 7}
+        sub.backward(dOut, stream, parts=lambda name: rec(marks[name]))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(8)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall * 1e3 / args.steps
+    phase = {n: sorted(e[i].elapsed_time(e[i + 1]) for e in events)[args.steps // 2] for i, n in enumerate(names)}
+    attn = phase["attn_fwd"] + phase["attn_bwd"]
+    total_events = sum(phase.values())
+    gemm_flop = 12 * 2.0 * B * T * C * C
+    attn_flop = 7.0 * B * H * T * T * D
+    result = {
+        "metric": "attention sublayer fwd+bwd ms per step (config 4), with the attention share",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config4: pre-LN attention sublayer fwd+bwd (QKV, causal flash attention, "
+                               "projection; their gradients)", "B": B, "T": T, "C": C, "H": H, "D": D},
+        "attention_share": round(attn / total_events, 4),
+        "phases_ms_median": {k: round(v, 4) for k, v in phase.items()},
+        "tflops": {"step": round((gemm_flop + attn_flop) / (ms * 1e-3) / 1e12, 2),
+                   "gemms": round(gemm_flop / ((total_events - attn - phase["zero"]) * 1e-3) / 1e12, 2),
+                   "attention": round(attn_flop / (attn * 1e-3) / 1e12, 2)},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4],
+                    help="1-3: attention core (fwd + computeD + bwd); 4: the whole attention sublayer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -100,6 +176,8 @@ def main():
     import torch
     import metalllm_amd as M
 
+    if args.config == 4:
+        return bench_sublayer(args)
     B, H, T, D, qk_scale, desc = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)

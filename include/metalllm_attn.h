@@ -54,7 +54,8 @@ enum {
   METALLLM_ATTN_E_LAYOUT = -4,   /* N != NH * D, NH == 0 or B == 0 */
   METALLLM_ATTN_E_SIZE = -5,     /* a tensor exceeds 2^31 elements */
   METALLLM_ATTN_E_ALIGN = -6,    /* a tensor pointer is not 16-byte aligned */
-  METALLLM_ATTN_E_LAUNCH = -7    /* the kernel launch failed */
+  METALLLM_ATTN_E_LAUNCH = -7,   /* the kernel launch failed */
+  METALLLM_ATTN_E_LIBRARY = -8   /* a platform library call (rocBLAS, device allocation) failed */
 };
 
 /* Replaces the flashAttentionForward dispatch at model.h:459-473 (attention.metal:56-164).
@@ -73,6 +74,44 @@ int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionPar
 int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                            const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                            const AttentionParams* p, metalllm_stream_t stream);
+
+/* ---- The sublayer around the attention core (attention.metal:19-53, 301-455) ----
+ * Plain GEMMs with the reference kernels' names and buffer order. Row-major: X, attn_out (O), dZ,
+ * q, k, v, dK, dV, dAttn, out are bf16 [B*M, N]; dQ and dX are fp32 [B*M, N]; weights (q_w, k_w,
+ * v_w, proj_w and their gradients) are bf16 [N, N] indexed [input feature][output feature], dQw
+ * fp32 [N, N]. Products are computed with fp32 accumulation (rocBLAS gemm_ex) and rounded once to
+ * the destination type. The "accumulate" kernels read their destination once and add to it, as
+ * the reference's multiply_accumulate matmuls do; the caller zeroes those destinations first
+ * (model.h:549-555). Validation: M, B, NH, D >= 1, N == NH*D, tensors below 2^31 elements, non-NULL
+ * 16-byte aligned pointers. The first call on a device creates that device's rocBLAS handle;
+ * computeGradDx/Dw also keep a per-device buffer for the bf16 split of dQ (grown on demand), so
+ * two of those calls on one device must not overlap on different streams. Asynchronous on `stream`. */
+
+/* attention.metal:19-53, dispatched at model.h:446-457: q = X.q_w, k = X.k_w, v = X.v_w. */
+int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w, const uint16_t* k_w,
+               const uint16_t* v_w, const AttentionParams* p, metalllm_stream_t stream);
+
+/* attention.metal:385-405, model.h:474-482: out = attn_out.proj_w. */
+int projForward(const uint16_t* attn_out, const uint16_t* proj_w, uint16_t* out, const AttentionParams* p,
+                metalllm_stream_t stream);
+
+/* attention.metal:407-430, model.h:621-629: dProjw += attn_out^T.dZ (bf16, accumulated). */
+int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, const AttentionParams* p,
+                   metalllm_stream_t stream);
+
+/* attention.metal:432-455, model.h:630-638: dAttn = dZ.proj_w^T (bf16). */
+int projBackwarddX(const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, const AttentionParams* p,
+                   metalllm_stream_t stream);
+
+/* attention.metal:301-341, model.h:666-677: dX += dQ.q_w^T + dK.k_w^T + dV.v_w^T (fp32, accumulated;
+ * dQ is the fp32 accumulator flashAttentionBackward produced). */
+int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
+                  const uint16_t* dK, const uint16_t* dV, const AttentionParams* p, metalllm_stream_t stream);
+
+/* attention.metal:343-383, model.h:679-690: dQw += X^T.dQ (fp32), dKw += X^T.dK, dVw += X^T.dV (bf16);
+ * all accumulated. */
+int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
+                  uint16_t* dKw, uint16_t* dVw, const AttentionParams* p, metalllm_stream_t stream);
 
 /* Bench hook (no counterpart in the reference): launches one of the two kernels that
  * flashAttentionBackward runs, in this order, on `stream`: part 0 = dK/dV (key-block owners),

@@ -6,5 +6,7 @@ The product is libmetalllm_attn.so (C ABI in include/metalllm_attn.h); this pack
 from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, backward_part,
                         computeD, flashAttentionBackward, flashAttentionForward, library, work_map)
 
-__all__ = ["AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
+from . import sublayer  # noqa: E402  (the GEMMs around the attention core)
+
+__all__ = ["sublayer", "AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
            "computeD", "flashAttentionBackward", "flashAttentionForward", "library", "work_map"]

@@ -20,9 +20,11 @@ LIB_PATH = os.path.join(PKG, "libmetalllm_attn.so")
 OK = 0
 ERRORS = {
     -1: "E_NULL", -2: "E_SEQLEN", -3: "E_HEADDIM", -4: "E_LAYOUT", -5: "E_SIZE", -6: "E_ALIGN", -7: "E_LAUNCH",
+    -8: "E_LIBRARY",
 }
 EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
-            "metalllmAttnErrorString", "metalllmAttnWorkMap")
+            "metalllmAttnErrorString", "metalllmAttnWorkMap", "computeQKV", "projForward", "projBackwarddW",
+            "projBackwarddX", "computeGradDx", "computeGradDw")
 
 
 class AttentionParams(ctypes.Structure):

@@ -16,7 +16,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmetalllm_attn.so")
-SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_computed.hip"]
+SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_computed.hip", "sublayer.hip"]
+LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]  # sublayer GEMMs
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -58,7 +59,7 @@ def build(stats: bool = False, verbose: bool = False) -> str:
             cmd += ["-Rpass-analysis=kernel-resource-usage"]
         logs.append(_run(cmd + [os.path.join(CSRC, src), "-o", obj]))
         objs.append(obj)
-    logs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"]))
+    logs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, *LIBS, "-o", LIB + ".tmp"]))
     os.replace(LIB + ".tmp", LIB)
     if stats or verbose:
         print("\n".join(l for l in logs if l))

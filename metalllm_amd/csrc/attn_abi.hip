@@ -81,6 +81,7 @@ const char* metalllmAttnErrorString(int code) {
     case METALLLM_ATTN_E_SIZE: return "a tensor exceeds 2^31 elements";
     case METALLLM_ATTN_E_ALIGN: return "tensor pointers must be 16-byte aligned";
     case METALLLM_ATTN_E_LAUNCH: return "kernel launch failed";
+    case METALLLM_ATTN_E_LIBRARY: return "platform library call (rocBLAS, device allocation) failed";
     default: return "unknown error";
   }
 }

@@ -1,0 +1,236 @@
+// sublayer.hip -- the GEMMs of metalLLM's attention sublayer around the attention core, as extern "C"
+// entry points with the reference kernels' names and buffer order (declared in
+// include/metalllm_attn.h):
+//   computeQKV      attention.metal:19-53   Q,K,V = X.Wq, X.Wk, X.Wv                       (bf16)
+//   projForward     attention.metal:385-405 out = O.Wp                                    (bf16)
+//   projBackwarddW  attention.metal:407-430 dWp += O^T.dZ                       (bf16, accumulated)
+//   projBackwarddX  attention.metal:432-455 dO = dZ.Wp^T                                   (bf16)
+//   computeGradDx   attention.metal:301-341 dX += dQ.Wq^T + dK.Wk^T + dV.Wv^T   (fp32, accumulated)
+//   computeGradDw   attention.metal:343-383 dWq += X^T.dQ (fp32), dWk += X^T.dK, dWv += X^T.dV (bf16)
+// Row-major matrices: X, O, dZ, Q, K, V, dK, dV bf16 [R, C] and dQ, dX fp32 [R, C] with R = B*M rows
+// and C = N = NH*D features; weights bf16 [C, C] indexed [input feature][output feature].
+//
+// These are plain GEMMs (no fused epilogue), so they run on the platform library: rocBLAS
+// gemm_ex with bf16 operands, fp32 accumulation and a bf16 or fp32 destination (beta = 1 for the
+// reference's multiply_accumulate kernels: the destination is read once and the sum rounded once).
+// The one operand the library cannot take as is, the fp32 dQ read by computeGradDx/Dw, is split by
+// a HIP kernel into two bf16 terms, dQ = hi + lo + O(2^-16 |dQ|), and each product runs twice:
+// the fp32 dQ never makes a bf16 round trip of its own.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/metalllm_attn.h"
+
+namespace {
+
+int validate_gemm(const AttentionParams* p) {
+  if (!p) return METALLLM_ATTN_E_NULL;
+  if (p->M == 0) return METALLLM_ATTN_E_SEQLEN;
+  if (p->NH == 0 || p->B == 0 || p->D == 0 || (uint64_t)p->N != (uint64_t)p->NH * p->D) return METALLLM_ATTN_E_LAYOUT;
+  if ((uint64_t)p->B * p->M * p->N >= (1ull << 31) || (uint64_t)p->N * p->N >= (1ull << 31)) return METALLLM_ATTN_E_SIZE;
+  return METALLLM_ATTN_OK;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// Per-device library state: the rocBLAS handle (created on first use with that device current)
+// and the bf16 split of dQ (grown on demand). A mutex per device serialises the host side of a
+// call (stream binding and enqueue) and the use of the split buffer: calls that read dQ
+// (computeGradDx, computeGradDw) on different streams of one device must not overlap.
+struct DeviceState {
+  std::mutex mu;
+  rocblas_handle handle = nullptr;
+  uint16_t* split = nullptr;  // hi [R*C] then lo [R*C]
+  size_t split_elems = 0;
+};
+
+DeviceState& state(int dev) {
+  static std::mutex table_mu;
+  static std::vector<DeviceState*> table;
+  std::lock_guard<std::mutex> g(table_mu);
+  if ((int)table.size() <= dev) table.resize(dev + 1, nullptr);
+  if (!table[dev]) table[dev] = new DeviceState();  // lives until the process ends
+  return *table[dev];
+}
+
+// Locks the current device's state and binds its handle to `stream`; null handle on failure.
+struct Session {
+  std::unique_lock<std::mutex> lock;
+  DeviceState* st = nullptr;
+  int rc = METALLLM_ATTN_OK;
+
+  explicit Session(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+      rc = METALLLM_ATTN_E_LIBRARY;
+      return;
+    }
+    st = &state(dev);
+    lock = std::unique_lock<std::mutex>(st->mu);
+    if (!st->handle && rocblas_create_handle(&st->handle) != rocblas_status_success) {
+      st->handle = nullptr;
+      rc = METALLLM_ATTN_E_LIBRARY;
+      return;
+    }
+    if (rocblas_set_stream(st->handle, stream) != rocblas_status_success) rc = METALLLM_ATTN_E_LIBRARY;
+  }
+};
+
+// Row-major C[M][N] = op(A)[M][K] . op(B)[K][N] + beta * C. op(A) = A stored [M][K] (lda) or, with
+// ta, A^T of A stored [K][M]; likewise op(B). rocBLAS is column-major: the row-major product is
+// computed as C^T = op(B)^T . op(A)^T on the same memory.
+int gemm_rm(rocblas_handle h, bool ta, bool tb, int M, int N, int K, const void* A, rocblas_datatype at, int lda,
+            const void* B, rocblas_datatype bt, int ldb, float beta, void* C, rocblas_datatype ct, int ldc) {
+  const float alpha = 1.0f;
+  const rocblas_status s = rocblas_gemm_ex(
+      h, tb ? rocblas_operation_transpose : rocblas_operation_none, ta ? rocblas_operation_transpose : rocblas_operation_none,
+      N, M, K, &alpha, B, bt, ldb, A, at, lda, &beta, C, ct, ldc, C, ct, ldc, rocblas_datatype_f32_r,
+      rocblas_gemm_algo_standard, 0, 0);
+  return s == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
+}
+
+constexpr rocblas_datatype BF = rocblas_datatype_bf16_r;
+constexpr rocblas_datatype F32 = rocblas_datatype_f32_r;
+
+__device__ __forceinline__ uint16_t rne_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);  // finite inputs
+}
+
+// hi = bf16(x), lo = bf16(x - hi): four elements per thread (16-byte loads).
+__global__ void __launch_bounds__(256) split_kernel(const float4* __restrict__ x, uint2* __restrict__ hi,
+                                                    uint2* __restrict__ lo, size_t n4) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    const float4 v = x[i];
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h[j] = rne_bf16(f[j]);
+      l[j] = rne_bf16(f[j] - __uint_as_float((uint32_t)h[j] << 16));
+    }
+    hi[i] = uint2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+    lo[i] = uint2{(uint32_t)l[0] | ((uint32_t)l[1] << 16), (uint32_t)l[2] | ((uint32_t)l[3] << 16)};
+  }
+}
+
+// Splits dQ [R*C] into the device's split buffer on `stream`; returns hi (lo follows at + R*C).
+int split_dq(DeviceState& st, const float* dQ, size_t elems, hipStream_t stream, const uint16_t** hi,
+             const uint16_t** lo) {
+  if (st.split_elems < elems) {
+    if (st.split) {
+      if (hipDeviceSynchronize() != hipSuccess || hipFree(st.split) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
+      st.split = nullptr;
+      st.split_elems = 0;
+    }
+    if (hipMalloc((void**)&st.split, 2 * elems * sizeof(uint16_t)) != hipSuccess) {
+      st.split = nullptr;
+      return METALLLM_ATTN_E_LIBRARY;
+    }
+    st.split_elems = elems;
+  }
+  const size_t n4 = elems / 4;  // C = NH*D is a multiple of 4 for every D this library accepts
+  const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 65536);
+  hipLaunchKernelGGL(split_kernel, dim3(blocks), dim3(256), 0, stream, (const float4*)dQ, (uint2*)st.split,
+                     (uint2*)(st.split + elems), n4);
+  if (hipGetLastError() != hipSuccess) return METALLLM_ATTN_E_LAUNCH;
+  *hi = st.split;
+  *lo = st.split + elems;
+  return METALLLM_ATTN_OK;
+}
+
+#define TRY(x)                  \
+  do {                          \
+    const int rc_ = (x);        \
+    if (rc_) return rc_;        \
+  } while (0)
+
+#define CHECK_PTRS(...)                                           \
+  do {                                                            \
+    const void* ps_[] = {__VA_ARGS__};                            \
+    for (const void* q_ : ps_) {                                  \
+      if (!q_) return METALLLM_ATTN_E_NULL;                       \
+      if (!aligned16(q_)) return METALLLM_ATTN_E_ALIGN;           \
+    }                                                             \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w, const uint16_t* k_w,
+               const uint16_t* v_w, const AttentionParams* p, metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(X, q, k, v, q_w, k_w, v_w);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  TRY(gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, q_w, BF, C, 0.0f, q, BF, C));
+  TRY(gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, k_w, BF, C, 0.0f, k, BF, C));
+  return gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, v_w, BF, C, 0.0f, v, BF, C);
+}
+
+int projForward(const uint16_t* attn_out, const uint16_t* proj_w, uint16_t* out, const AttentionParams* p,
+                metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(attn_out, proj_w, out);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  return gemm_rm(s.st->handle, false, false, R, C, C, attn_out, BF, C, proj_w, BF, C, 0.0f, out, BF, C);
+}
+
+int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, const AttentionParams* p,
+                   metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(attn_out, dZ, dProjw);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  return gemm_rm(s.st->handle, true, false, C, C, R, attn_out, BF, C, dZ, BF, C, 1.0f, dProjw, BF, C);
+}
+
+int projBackwarddX(const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, const AttentionParams* p,
+                   metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(dZ, proj_w, dAttn);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  return gemm_rm(s.st->handle, false, true, R, C, C, dZ, BF, C, proj_w, BF, C, 0.0f, dAttn, BF, C);
+}
+
+int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
+                  const uint16_t* dK, const uint16_t* dV, const AttentionParams* p, metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(dX, qw, kw, vw, dQ, dK, dV);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  const uint16_t *hi = nullptr, *lo = nullptr;
+  TRY(split_dq(*s.st, dQ, (size_t)R * C, (hipStream_t)stream, &hi, &lo));
+  TRY(gemm_rm(s.st->handle, false, true, R, C, C, hi, BF, C, qw, BF, C, 1.0f, dX, F32, C));
+  TRY(gemm_rm(s.st->handle, false, true, R, C, C, lo, BF, C, qw, BF, C, 1.0f, dX, F32, C));
+  TRY(gemm_rm(s.st->handle, false, true, R, C, C, dK, BF, C, kw, BF, C, 1.0f, dX, F32, C));
+  return gemm_rm(s.st->handle, false, true, R, C, C, dV, BF, C, vw, BF, C, 1.0f, dX, F32, C);
+}
+
+int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
+                  uint16_t* dKw, uint16_t* dVw, const AttentionParams* p, metalllm_stream_t stream) {
+  TRY(validate_gemm(p));
+  CHECK_PTRS(x, dQ, dK, dV, dQw, dKw, dVw);
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Session s((hipStream_t)stream);
+  TRY(s.rc);
+  const uint16_t *hi = nullptr, *lo = nullptr;
+  TRY(split_dq(*s.st, dQ, (size_t)R * C, (hipStream_t)stream, &hi, &lo));
+  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, hi, BF, C, 1.0f, dQw, F32, C));
+  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, lo, BF, C, 1.0f, dQw, F32, C));
+  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, dK, BF, C, 1.0f, dKw, BF, C));
+  return gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, dV, BF, C, 1.0f, dVw, BF, C);
+}
+
+}  // extern "C"

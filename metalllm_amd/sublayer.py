@@ -1,0 +1,135 @@
+"""Host side of the attention sublayer around the attention core: ctypes bindings of the six GEMM
+entry points of libmetalllm_attn.so (computeQKV, projForward, projBackwarddW, projBackwarddX,
+computeGradDx, computeGradDw; /root/reference/attention.metal:19-53, 301-455) and the sublayer's
+forward and backward chains in the order /root/reference/model.h:446-482 and :621-690 encode them.
+
+Tensors are torch tensors on the GPU, contiguous: activations [B, T, C] (or [R, C]) with C = H*D,
+weights [C, C] indexed [input feature][output feature]. No CPU fallback: every product runs on
+the device through the library.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from .attention import (AttentionParams, _check, _lib, _ptr, _stream, attention_forward, backward_part, computeD,
+                        flashAttentionForward)
+
+_BOUND = False
+
+
+def _L():
+    global _BOUND
+    L = _lib()
+    if not _BOUND:
+        vp = ctypes.c_void_p
+        pp = ctypes.POINTER(AttentionParams)
+        L.computeQKV.argtypes = [vp] * 7 + [pp, vp]
+        L.projForward.argtypes = [vp] * 3 + [pp, vp]
+        L.projBackwarddW.argtypes = [vp] * 3 + [pp, vp]
+        L.projBackwarddX.argtypes = [vp] * 3 + [pp, vp]
+        L.computeGradDx.argtypes = [vp] * 7 + [pp, vp]
+        L.computeGradDw.argtypes = [vp] * 7 + [pp, vp]
+        for f in (L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw):
+            f.restype = ctypes.c_int
+        _BOUND = True
+    return L
+
+
+def params_of(x, H: int) -> AttentionParams:
+    """AttentionParams of an activation [B, T, C] (or [R, C], taken as B = 1) with H heads."""
+    if x.dim() == 3:
+        B, T, C = x.shape
+    else:
+        (T, C), B = x.shape, 1
+    return AttentionParams.of(B, T, H, C // H)
+
+
+def computeQKV(X, q, k, v, q_w, k_w, v_w, p: AttentionParams, stream=None):
+    """attention.metal:19-53: q, k, v = X.q_w, X.k_w, X.v_w (bf16)."""
+    _check(_L().computeQKV(_ptr(X), _ptr(q), _ptr(k), _ptr(v), _ptr(q_w), _ptr(k_w), _ptr(v_w), ctypes.byref(p),
+                           _stream(stream)), "computeQKV")
+
+
+def projForward(attn_out, proj_w, out, p: AttentionParams, stream=None):
+    """attention.metal:385-405: out = attn_out.proj_w (bf16)."""
+    _check(_L().projForward(_ptr(attn_out), _ptr(proj_w), _ptr(out), ctypes.byref(p), _stream(stream)), "projForward")
+
+
+def projBackwarddW(attn_out, dZ, dProjw, p: AttentionParams, stream=None):
+    """attention.metal:407-430: dProjw += attn_out^T.dZ (bf16, accumulated)."""
+    _check(_L().projBackwarddW(_ptr(attn_out), _ptr(dZ), _ptr(dProjw), ctypes.byref(p), _stream(stream)),
+           "projBackwarddW")
+
+
+def projBackwarddX(dZ, proj_w, dAttn, p: AttentionParams, stream=None):
+    """attention.metal:432-455: dAttn = dZ.proj_w^T (bf16)."""
+    _check(_L().projBackwarddX(_ptr(dZ), _ptr(proj_w), _ptr(dAttn), ctypes.byref(p), _stream(stream)),
+           "projBackwarddX")
+
+
+def computeGradDx(dX, qw, kw, vw, dQ, dK, dV, p: AttentionParams, stream=None):
+    """attention.metal:301-341: dX += dQ.qw^T + dK.kw^T + dV.vw^T (fp32, accumulated)."""
+    _check(_L().computeGradDx(_ptr(dX), _ptr(qw), _ptr(kw), _ptr(vw), _ptr(dQ), _ptr(dK), _ptr(dV), ctypes.byref(p),
+                              _stream(stream)), "computeGradDx")
+
+
+def computeGradDw(x, dQ, dK, dV, dQw, dKw, dVw, p: AttentionParams, stream=None):
+    """attention.metal:343-383: dQw += x^T.dQ (fp32); dKw, dVw += x^T.dK, x^T.dV (bf16); accumulated."""
+    _check(_L().computeGradDw(_ptr(x), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dQw), _ptr(dKw), _ptr(dVw),
+                              ctypes.byref(p), _stream(stream)), "computeGradDw")
+
+
+class Sublayer:
+    """Buffers and launch sequence of one attention sublayer (pre-LN block, without the layernorm
+    and residual glue), mirroring model.h: forward computeQKV -> flashAttentionForward ->
+    projForward (model.h:446-482); backward projBackwarddW, projBackwarddX, computeD,
+    flashAttentionBackward, computeGradDx, computeGradDw (model.h:621-690), with the gradient
+    buffers zeroed first as model.h:549-555 does."""
+
+    def __init__(self, X, Wq, Wk, Wv, Wp, H: int):
+        import torch
+        self.X, self.Wq, self.Wk, self.Wv, self.Wp, self.H = X, Wq, Wk, Wv, Wp, H
+        B, T, C = X.shape
+        self.p = params_of(X, H)
+        D = C // H
+        dev = X.device
+        bf = lambda: torch.empty((B, T, C), dtype=torch.bfloat16, device=dev)
+        self.q, self.k, self.v, self.o, self.out = bf(), bf(), bf(), bf(), bf()
+        self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        self.dO, self.dK, self.dV = bf(), bf(), bf()
+        self.Dv = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        self.dQ = torch.zeros((B, T, C), dtype=torch.float32, device=dev)
+        self.dX = torch.zeros((B, T, C), dtype=torch.float32, device=dev)
+        self.dWq = torch.zeros((C, C), dtype=torch.float32, device=dev)
+        self.dWk = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
+        self.dWv = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
+        self.dWp = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
+        self.D = D
+
+    def forward(self, stream=None):
+        p = self.p
+        computeQKV(self.X, self.q, self.k, self.v, self.Wq, self.Wk, self.Wv, p, stream)
+        flashAttentionForward(self.q, self.k, self.v, self.o, self.lse, stream, p)
+        projForward(self.o, self.Wp, self.out, p, stream)
+        return self.out
+
+    def zero_grads(self):
+        for t in (self.dQ, self.dX, self.dWq, self.dWk, self.dWv, self.dWp):
+            t.zero_()
+
+    def backward(self, dOut, stream=None, parts=None):
+        """dOut: gradient at the sublayer output [B, T, C] bf16. `parts`, if given, is a list of
+        (name, callable) hooks run between launches (the bench records events there)."""
+        p = self.p
+        mark = (lambda name: parts(name)) if parts else (lambda name: None)
+        projBackwarddW(self.o, dOut, self.dWp, p, stream)
+        projBackwarddX(dOut, self.Wp, self.dO, p, stream)
+        mark("proj")
+        computeD(self.dO, self.o, self.Dv, stream, p)
+        backward_part(0, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p)
+        backward_part(1, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p)
+        mark("attention")
+        computeGradDx(self.dX, self.Wq, self.Wk, self.Wv, self.dQ, self.dK, self.dV, p, stream)
+        computeGradDw(self.X, self.dQ, self.dK, self.dV, self.dWq, self.dWk, self.dWv, p, stream)
+        mark("grads")
+        return self.dX

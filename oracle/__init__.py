@@ -170,3 +170,83 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
     return u.astype(np.uint16)
+
+
+# ---- sublayer GEMMs (gemm_oracle.cpp): row-major, R = B*T rows, C = NH*D features ----
+T_BF16, T_F32 = 0, 1
+_GEMM_BOUND = False
+
+
+def _gemm_lib():
+    global _GEMM_BOUND
+    L = lib()
+    if not _GEMM_BOUND:
+        vp = ctypes.c_void_p
+        i = ctypes.c_int
+        L.oracle_gemm.argtypes = [i, i, i, i, i, vp, i, i, vp, i, i, vp, i, i, i, i]
+        L.oracle_computeQKV.argtypes = [vp] * 7 + [i, i, i]
+        L.oracle_projForward.argtypes = [vp] * 3 + [i, i, i]
+        L.oracle_projBackwarddW.argtypes = [vp] * 3 + [i, i, i]
+        L.oracle_projBackwarddX.argtypes = [vp] * 3 + [i, i, i]
+        L.oracle_computeGradDx.argtypes = [vp] * 7 + [i, i, i]
+        L.oracle_computeGradDw.argtypes = [vp] * 7 + [i, i, i]
+        _GEMM_BOUND = True
+    return L
+
+
+def _p(x: np.ndarray):
+    assert x.flags["C_CONTIGUOUS"]
+    return x.ctypes.data_as(ctypes.c_void_p)
+
+
+def gemm(A, B, C, ta=False, tb=False, accumulate=False, threads=0):
+    """C (=|+=) op(A) . op(B), row-major; A/B/C uint16 (bf16 bits) or float32 numpy arrays."""
+    M, N = C.shape
+    K = A.shape[0] if ta else A.shape[1]
+    t = lambda x: T_BF16 if x.dtype == np.uint16 else T_F32
+    rc = _gemm_lib().oracle_gemm(int(ta), int(tb), M, N, K, _p(A), t(A), A.shape[1], _p(B), t(B), B.shape[1], _p(C),
+                                 t(C), C.shape[1], int(accumulate), threads)
+    _check(rc, "gemm")
+    return C
+
+
+def computeQKV(X, qw, kw, vw, threads=0):
+    R, Cf = X.shape
+    q, k, v = (np.zeros((R, Cf), np.uint16) for _ in range(3))
+    _gemm_lib().oracle_computeQKV(_p(X), _p(q), _p(k), _p(v), _p(qw), _p(kw), _p(vw), R, Cf, threads)
+    return q, k, v
+
+
+def projForward(attn_out, proj_w, threads=0):
+    R, Cf = attn_out.shape
+    out = np.zeros((R, Cf), np.uint16)
+    _gemm_lib().oracle_projForward(_p(attn_out), _p(proj_w), _p(out), R, Cf, threads)
+    return out
+
+
+def projBackwarddW(attn_out, dZ, dProjw, threads=0):
+    """dProjw (bf16, accumulated into) += O^T . dZ."""
+    R, Cf = attn_out.shape
+    _gemm_lib().oracle_projBackwarddW(_p(attn_out), _p(dZ), _p(dProjw), R, Cf, threads)
+    return dProjw
+
+
+def projBackwarddX(dZ, proj_w, threads=0):
+    R, Cf = dZ.shape
+    dAttn = np.zeros((R, Cf), np.uint16)
+    _gemm_lib().oracle_projBackwarddX(_p(dZ), _p(proj_w), _p(dAttn), R, Cf, threads)
+    return dAttn
+
+
+def computeGradDx(dX, qw, kw, vw, dQ, dK, dV, threads=0):
+    """dX (fp32, accumulated into) += dQ.Wq^T + dK.Wk^T + dV.Wv^T (three accumulate runs)."""
+    R, Cf = dX.shape
+    _gemm_lib().oracle_computeGradDx(_p(dX), _p(qw), _p(kw), _p(vw), _p(dQ), _p(dK), _p(dV), R, Cf, threads)
+    return dX
+
+
+def computeGradDw(x, dQ, dK, dV, dQw, dKw, dVw, threads=0):
+    """dQw (fp32) += X^T.dQ; dKw, dVw (bf16) += X^T.dK, X^T.dV."""
+    R, Cf = x.shape
+    _gemm_lib().oracle_computeGradDw(_p(x), _p(dQ), _p(dK), _p(dV), _p(dQw), _p(dKw), _p(dVw), R, Cf, threads)
+    return dQw, dKw, dVw

@@ -74,3 +74,29 @@ def test_error_strings():
     lib = M.library()
     for code in range(-7, 1):
         assert lib.metalllmAttnErrorString(code)
+
+
+GEMM_ARGS = {  # entry point -> number of tensor pointers before the params pointer
+    "computeQKV": 7, "projForward": 3, "projBackwarddW": 3, "projBackwarddX": 3, "computeGradDx": 7, "computeGradDw": 7,
+}
+
+
+@pytest.mark.parametrize("name", sorted(GEMM_ARGS))
+def test_sublayer_gemms_validate_before_device(name):
+    """The sublayer GEMM entry points reject bad shapes, NULL and misaligned pointers without a
+    device call (M = 0, N != NH*D, oversized tensors; D is free: these are plain GEMMs)."""
+    lib = M.library()
+    f = getattr(lib, name)
+    n = GEMM_ARGS[name]
+    ok = ctypes.c_void_p(1 << 20)
+    good = dict(M=256, N=384, D=64, NH=6, B=1)
+    for change, code in ((dict(M=0), -2), (dict(N=383), -4), (dict(NH=0, N=0), -4), (dict(B=0), -4),
+                         (dict(B=1 << 12, M=1 << 16), -5)):
+        g = dict(good)
+        g.update(change)
+        p = AttentionParams(g["M"], g["N"], g["D"], g["NH"], g["B"])
+        assert f(*([ok] * n), ctypes.byref(p), None) == code, (name, change)
+    p = AttentionParams(256, 384, 64, 6, 1)
+    assert f(*([ok] * (n - 1)), None, ctypes.byref(p), None) == -1
+    assert f(*([ok] * (n - 1)), ctypes.c_void_p((1 << 20) + 4), ctypes.byref(p), None) == -6
+    assert f(*([ok] * n), None, None) == -1

@@ -1,0 +1,156 @@
+"""GPU parity of the sublayer GEMMs (computeQKV, projForward, projBackwarddW, projBackwarddX,
+computeGradDx, computeGradDw) through the C ABI against the CPU oracle (oracle/gemm_oracle.cpp).
+
+Bars: bf16 destinations within one bf16 ulp of the oracle's value plus 1e-5 of max|ref| (the
+library sums in another order than the oracle's sequential fp32 sum, which can move a result across
+a bf16 rounding boundary); fp32 destinations within 1e-4 of max|ref| (summation order, plus the
+two-term bf16 split of the fp32 dQ operand, |dQ - hi - lo| <= 2^-17 |dQ|).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.attn_case import bf16_ulp, f32, to_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def bf_err(gpu, ref):
+    a, b = f32(gpu), f32(ref)
+    d = np.abs(a - b)
+    bar = bf16_ulp(b) + 1e-5 * np.abs(b).max()
+    return int((d > bar).sum()), float(d.max())
+
+
+def f32_err(gpu, ref):
+    return float(np.abs(gpu - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def inputs(R, C, seed):
+    rng = np.random.default_rng(seed)
+    X = O.f32_to_bf16(rng.standard_normal((R, C)).astype(np.float32))
+    W = [O.f32_to_bf16((rng.standard_normal((C, C)) * 0.02).astype(np.float32)) for _ in range(4)]
+    return X, W
+
+
+@pytest.fixture(scope="module")
+def S():
+    import metalllm_amd.sublayer as S
+    return S
+
+
+def test_forward_gemms(gpu, S):
+    import torch
+    B, T, H, C = 2, 256, 12, 768
+    R = B * T
+    X, (Wq, Wk, Wv, Wp) = inputs(R, C, 1)
+    p = S.params_of(torch.empty((B, T, C)), H)
+    tX, tq_w, tk_w, tv_w, tWp = (to_gpu(a, gpu) for a in (X, Wq, Wk, Wv, Wp))
+    q, k, v = (torch.empty((R, C), dtype=torch.bfloat16, device=gpu) for _ in range(3))
+    S.computeQKV(tX, q, k, v, tq_w, tk_w, tv_w, p)
+    out = torch.empty((R, C), dtype=torch.bfloat16, device=gpu)
+    S.projForward(q, tWp, out, p)
+    rq, rk, rv = O.computeQKV(X, Wq, Wk, Wv, threads=16)
+    for name, g, r in (("q", q, rq), ("k", k, rk), ("v", v, rv)):
+        bad, mx = bf_err(to_np(g), r)
+        print(f"computeQKV {name}: beyond bar {bad}, max err {mx:.3g}")
+        assert bad == 0
+    rout = O.projForward(to_np(q), Wp, threads=16)
+    bad, mx = bf_err(to_np(out), rout)
+    print(f"projForward: beyond bar {bad}, max err {mx:.3g}")
+    assert bad == 0
+
+
+def test_backward_gemms(gpu, S):
+    import torch
+    B, T, H, C = 2, 256, 12, 768
+    R = B * T
+    X, (Wq, Wk, Wv, Wp) = inputs(R, C, 2)
+    rng = np.random.default_rng(3)
+    dZ = O.f32_to_bf16(rng.standard_normal((R, C)).astype(np.float32))
+    dK = O.f32_to_bf16((rng.standard_normal((R, C)) * 0.1).astype(np.float32))
+    dV = O.f32_to_bf16((rng.standard_normal((R, C)) * 0.1).astype(np.float32))
+    dQ = (rng.standard_normal((R, C)) * 0.1).astype(np.float32)
+    p = S.params_of(torch.empty((B, T, C)), H)
+    g = {n: to_gpu(a, gpu) for n, a in dict(X=X, Wq=Wq, Wk=Wk, Wv=Wv, Wp=Wp, dZ=dZ, dK=dK, dV=dV, dQ=dQ).items()}
+    # projBackwarddW twice: the destination is accumulated into (bf16(bf16(S) + S))
+    dWp = torch.zeros((C, C), dtype=torch.bfloat16, device=gpu)
+    S.projBackwarddW(g["X"], g["dZ"], dWp, p)
+    S.projBackwarddW(g["X"], g["dZ"], dWp, p)
+    rWp = O.projBackwarddW(X, dZ, np.zeros((C, C), np.uint16), threads=16)
+    rWp = O.projBackwarddW(X, dZ, rWp, threads=16)
+    bad, mx = bf_err(to_np(dWp), rWp)
+    print(f"projBackwarddW x2: beyond bar {bad}, max err {mx:.3g}")
+    assert bad == 0
+    dA = torch.empty((R, C), dtype=torch.bfloat16, device=gpu)
+    S.projBackwarddX(g["dZ"], g["Wp"], dA, p)
+    bad, mx = bf_err(to_np(dA), O.projBackwarddX(dZ, Wp, threads=16))
+    print(f"projBackwarddX: beyond bar {bad}, max err {mx:.3g}")
+    assert bad == 0
+    dX0 = (rng.standard_normal((R, C)) * 0.01).astype(np.float32)  # nonzero: accumulated into
+    dX = to_gpu(dX0, gpu)
+    S.computeGradDx(dX, g["Wq"], g["Wk"], g["Wv"], g["dQ"], g["dK"], g["dV"], p)
+    rX = O.computeGradDx(dX0.copy(), Wq, Wk, Wv, dQ, dK, dV, threads=16)
+    e = f32_err(to_np(dX), rX)
+    print(f"computeGradDx: rel-to-max {e:.3g}")
+    assert e <= 1e-4
+    dQw = torch.zeros((C, C), dtype=torch.float32, device=gpu)
+    dKw = torch.zeros((C, C), dtype=torch.bfloat16, device=gpu)
+    dVw = torch.zeros((C, C), dtype=torch.bfloat16, device=gpu)
+    S.computeGradDw(g["X"], g["dQ"], g["dK"], g["dV"], dQw, dKw, dVw, p)
+    rQw, rKw, rVw = O.computeGradDw(X, dQ, dK, dV, np.zeros((C, C), np.float32), np.zeros((C, C), np.uint16),
+                                    np.zeros((C, C), np.uint16), threads=16)
+    e = f32_err(to_np(dQw), rQw)
+    print(f"computeGradDw dQw: rel-to-max {e:.3g}")
+    assert e <= 1e-4
+    for name, t, r in (("dKw", dKw, rKw), ("dVw", dVw, rVw)):
+        bad, mx = bf_err(to_np(t), r)
+        print(f"computeGradDw {name}: beyond bar {bad}, max err {mx:.3g}")
+        assert bad == 0
+
+
+def test_config4_sublayer_chain(gpu, S):
+    """Config 4's sublayer (C=768, H=12, D=64, T=2048) at B=1: the model.h launch sequence on the GPU;
+    every stage checked against the oracle on the GPU's own inputs to that stage (attention by the
+    bars of the attention parity tests)."""
+    import torch
+    B, T, H, C = 1, 2048, 12, 768
+    R = B * T
+    X, (Wq, Wk, Wv, Wp) = inputs(R, C, 4)
+    rng = np.random.default_rng(5)
+    dOut = O.f32_to_bf16(rng.standard_normal((R, C)).astype(np.float32))
+    tX = to_gpu(X.reshape(B, T, C), gpu)
+    Ws = [to_gpu(w, gpu) for w in (Wq, Wk, Wv, Wp)]
+    sub = S.Sublayer(tX, *Ws, H=H)
+    sub.zero_grads()
+    out = sub.forward()
+    sub.backward(to_gpu(dOut.reshape(B, T, C), gpu))
+    torch.cuda.synchronize()
+    n = lambda t: to_np(t).reshape(R, C) if t.dim() == 3 else to_np(t)
+    # forward stages
+    rq, rk, rv = O.computeQKV(X, Wq, Wk, Wv, threads=16)
+    for g, r in ((sub.q, rq), (sub.k, rk), (sub.v, rv)):
+        assert bf_err(n(g), r)[0] == 0
+    q4 = lambda a: np.ascontiguousarray(a.reshape(B, T, H, C // H))
+    r_o, r_lse = O.forward(q4(n(sub.q)), q4(n(sub.k)), q4(n(sub.v)), O.opts(threads=16))
+    assert float(np.abs(to_np(sub.lse) - r_lse).max()) <= 1e-3
+    assert float(np.abs(f32(n(sub.o)) - f32(r_o.reshape(R, C))).max()) <= 1e-2
+    assert bf_err(n(out), O.projForward(n(sub.o), Wp, threads=16))[0] == 0
+    # backward stages
+    rWp = O.projBackwarddW(n(sub.o), dOut, np.zeros((C, C), np.uint16), threads=16)
+    assert bf_err(to_np(sub.dWp), rWp)[0] == 0
+    assert bf_err(n(sub.dO), O.projBackwarddX(dOut, Wp, threads=16))[0] == 0
+    rD = O.compute_d(q4(n(sub.dO)), q4(n(sub.o)))
+    assert np.array_equal(to_np(sub.Dv), rD)
+    rQ, rK, rV = O.backward(q4(n(sub.dO)), rD, to_np(sub.lse), q4(n(sub.q)), q4(n(sub.k)), q4(n(sub.v)),
+                            O.opts(threads=16))
+    for g, r in ((sub.dQ, rQ), (sub.dK, rK), (sub.dV, rV)):
+        a, b = f32(n(g)), f32(r.reshape(R, C))
+        assert float(np.abs(a - b).max() / np.abs(b).max()) <= 2e-2
+    rX = O.computeGradDx(np.zeros((R, C), np.float32), Wq, Wk, Wv, n(sub.dQ), n(sub.dK), n(sub.dV), threads=16)
+    assert f32_err(n(sub.dX), rX) <= 1e-4
+    rQw, rKw, rVw = O.computeGradDw(X, n(sub.dQ), n(sub.dK), n(sub.dV), np.zeros((C, C), np.float32),
+                                    np.zeros((C, C), np.uint16), np.zeros((C, C), np.uint16), threads=16)
+    assert f32_err(to_np(sub.dWq), rQw) <= 1e-4
+    assert bf_err(to_np(sub.dWk), rKw)[0] == 0
+    assert bf_err(to_np(sub.dWv), rVw)[0] == 0
