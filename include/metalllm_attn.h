@@ -82,10 +82,12 @@ int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, c
  * fp32 [N, N]. Products are computed with fp32 accumulation (rocBLAS gemm_ex) and rounded once to
  * the destination type. The "accumulate" kernels read their destination once and add to it, as
  * the reference's multiply_accumulate matmuls do; the caller zeroes those destinations first
- * (model.h:549-555). Validation: M, B, NH, D >= 1, N == NH*D, tensors below 2^31 elements, non-NULL
- * 16-byte aligned pointers. The first call on a device creates that device's rocBLAS handle;
- * computeGradDx/Dw also keep a per-device buffer for the bf16 split of dQ (grown on demand), so
- * two of those calls on one device must not overlap on different streams. Asynchronous on `stream`. */
+ * (model.h:549-555). Validation: M, B, NH, D >= 1, N == NH*D a multiple of 8, tensors below 2^31
+ * elements, non-NULL 16-byte aligned pointers. The first call on a device creates that device's
+ * rocBLAS handle; computeGradDx/Dw keep a per-device buffer for the two-term bf16 split of dQ, and
+ * projBackwarddW/computeGradDw one for fp32 partial sums of the weight gradients (both grown on
+ * demand and kept until the process ends), so those calls must not overlap on different streams
+ * of one device. Asynchronous on `stream`. */
 
 /* attention.metal:19-53, dispatched at model.h:446-457: q = X.q_w, k = X.k_w, v = X.v_w. */
 int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w, const uint16_t* k_w,

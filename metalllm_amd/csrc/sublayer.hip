@@ -29,23 +29,44 @@ namespace {
 int validate_gemm(const AttentionParams* p) {
   if (!p) return METALLLM_ATTN_E_NULL;
   if (p->M == 0) return METALLLM_ATTN_E_SEQLEN;
-  if (p->NH == 0 || p->B == 0 || p->D == 0 || (uint64_t)p->N != (uint64_t)p->NH * p->D) return METALLLM_ATTN_E_LAYOUT;
+  if (p->NH == 0 || p->B == 0 || p->D == 0 || (uint64_t)p->N != (uint64_t)p->NH * p->D || p->N % 8)
+    return METALLLM_ATTN_E_LAYOUT;  // rows of 16-byte multiples
   if ((uint64_t)p->B * p->M * p->N >= (1ull << 31) || (uint64_t)p->N * p->N >= (1ull << 31)) return METALLLM_ATTN_E_SIZE;
   return METALLLM_ATTN_OK;
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-// Per-device library state: the rocBLAS handle (created on first use with that device current)
-// and the bf16 split of dQ (grown on demand). A mutex per device serialises the host side of a
-// call (stream binding and enqueue) and the use of the split buffer: calls that read dQ
-// (computeGradDx, computeGradDw) on different streams of one device must not overlap.
+// Per-device library state: the rocBLAS handle (created on first use with that device current),
+// the bf16 split of dQ and the fp32 partials of the weight gradients (grown on demand). A mutex
+// per device serialises the host side of a call (stream binding and enqueue); the buffers are
+// shared, so computeGradDx, computeGradDw and projBackwarddW calls on different streams of one
+// device must not overlap.
 struct DeviceState {
   std::mutex mu;
   rocblas_handle handle = nullptr;
   uint16_t* split = nullptr;  // hi [R*C] then lo [R*C]
   size_t split_elems = 0;
+  float* partial = nullptr;   // fp32 partial products of the weight gradients [parts][C][C]
+  size_t partial_elems = 0;
 };
+
+// Grows a per-device buffer (never shrinks; the old one is freed after the device drained).
+template <typename T>
+int ensure(T*& buf, size_t& have, size_t need) {
+  if (have >= need) return METALLLM_ATTN_OK;
+  if (buf) {
+    if (hipDeviceSynchronize() != hipSuccess || hipFree(buf) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
+    buf = nullptr;
+    have = 0;
+  }
+  if (hipMalloc((void**)&buf, need * sizeof(T)) != hipSuccess) {
+    buf = nullptr;
+    return METALLLM_ATTN_E_LIBRARY;
+  }
+  have = need;
+  return METALLLM_ATTN_OK;
+}
 
 DeviceState& state(int dev) {
   static std::mutex table_mu;
@@ -120,19 +141,9 @@ __global__ void __launch_bounds__(256) split_kernel(const float4* __restrict__ x
 // Splits dQ [R*C] into the device's split buffer on `stream`; returns hi (lo follows at + R*C).
 int split_dq(DeviceState& st, const float* dQ, size_t elems, hipStream_t stream, const uint16_t** hi,
              const uint16_t** lo) {
-  if (st.split_elems < elems) {
-    if (st.split) {
-      if (hipDeviceSynchronize() != hipSuccess || hipFree(st.split) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
-      st.split = nullptr;
-      st.split_elems = 0;
-    }
-    if (hipMalloc((void**)&st.split, 2 * elems * sizeof(uint16_t)) != hipSuccess) {
-      st.split = nullptr;
-      return METALLLM_ATTN_E_LIBRARY;
-    }
-    st.split_elems = elems;
-  }
-  const size_t n4 = elems / 4;  // C = NH*D is a multiple of 4 for every D this library accepts
+  const int rc = ensure(st.split, st.split_elems, 2 * elems);
+  if (rc) return rc;
+  const size_t n4 = elems / 4;  // C is a multiple of 8 (validate_gemm)
   const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 65536);
   hipLaunchKernelGGL(split_kernel, dim3(blocks), dim3(256), 0, stream, (const float4*)dQ, (uint2*)st.split,
                      (uint2*)(st.split + elems), n4);
@@ -140,6 +151,53 @@ int split_dq(DeviceState& st, const float* dQ, size_t elems, hipStream_t stream,
   *hi = st.split;
   *lo = st.split + elems;
   return METALLLM_ATTN_OK;
+}
+
+// Weight gradients W[k][n] += sum_r X[r][k] G[r][n] reduce over all R rows into a small C x C
+// output: one GEMM gives the library too few output tiles for the chip. The rows are split into
+// `parts` chunks, computed as one strided-batched GEMM into fp32 partials [chunk][C][C], and
+// reduce_kernel adds the partials (of one or more such products) and the destination's previous
+// value once, then rounds to the destination type.
+int row_chunks(int R) {
+  for (int s : {16, 8, 4, 2})
+    if (R % s == 0 && R / s >= 512) return s;
+  return 1;
+}
+
+int xt_g_partials(rocblas_handle h, const uint16_t* X, const uint16_t* G, int R, int C, int parts, float* out) {
+  const float alpha = 1.0f, beta = 0.0f;
+  const int Rs = R / parts;
+  // row-major out_s[C][C] = X_s^T . G_s; column-major: out_s^T = G_s^T . X_s
+  const rocblas_status st = rocblas_gemm_strided_batched_ex(
+      h, rocblas_operation_none, rocblas_operation_transpose, C, C, Rs, &alpha, G, BF, C, (rocblas_stride)Rs * C, X, BF,
+      C, (rocblas_stride)Rs * C, &beta, out, F32, C, (rocblas_stride)C * C, out, F32, C, (rocblas_stride)C * C, parts,
+      rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  return st == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
+}
+
+// dst[i] = round(dst[i] + sum_p part[p * n + i]) with the fp32 sum in p order; dst fp32 or bf16.
+template <bool BF16_DST>
+__global__ void __launch_bounds__(256) reduce_kernel(const float* __restrict__ part, int nparts, size_t n, void* dst) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int p = 0; p < nparts; ++p) acc += part[(size_t)p * n + i];
+    if (BF16_DST) {
+      uint16_t* d = (uint16_t*)dst;
+      d[i] = rne_bf16(__uint_as_float((uint32_t)d[i] << 16) + acc);
+    } else {
+      float* d = (float*)dst;
+      d[i] = d[i] + acc;
+    }
+  }
+}
+
+int reduce_into(const float* part, int nparts, size_t n, void* dst, bool bf16_dst, hipStream_t stream) {
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  if (bf16_dst)
+    hipLaunchKernelGGL(reduce_kernel<true>, dim3(blocks), dim3(256), 0, stream, part, nparts, n, dst);
+  else
+    hipLaunchKernelGGL(reduce_kernel<false>, dim3(blocks), dim3(256), 0, stream, part, nparts, n, dst);
+  return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
 #define TRY(x)                  \
@@ -190,7 +248,10 @@ int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProj
   const int R = (int)(p->B * p->M), C = (int)p->N;
   Session s((hipStream_t)stream);
   TRY(s.rc);
-  return gemm_rm(s.st->handle, true, false, C, C, R, attn_out, BF, C, dZ, BF, C, 1.0f, dProjw, BF, C);
+  const int parts = row_chunks(R);
+  TRY(ensure(s.st->partial, s.st->partial_elems, (size_t)parts * C * C));
+  TRY(xt_g_partials(s.st->handle, attn_out, dZ, R, C, parts, s.st->partial));
+  return reduce_into(s.st->partial, parts, (size_t)C * C, dProjw, true, (hipStream_t)stream);
 }
 
 int projBackwarddX(const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, const AttentionParams* p,
@@ -227,10 +288,19 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
   TRY(s.rc);
   const uint16_t *hi = nullptr, *lo = nullptr;
   TRY(split_dq(*s.st, dQ, (size_t)R * C, (hipStream_t)stream, &hi, &lo));
-  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, hi, BF, C, 1.0f, dQw, F32, C));
-  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, lo, BF, C, 1.0f, dQw, F32, C));
-  TRY(gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, dK, BF, C, 1.0f, dKw, BF, C));
-  return gemm_rm(s.st->handle, true, false, C, C, R, x, BF, C, dV, BF, C, 1.0f, dVw, BF, C);
+  const int parts = row_chunks(R);
+  const size_t cc = (size_t)C * C;
+  TRY(ensure(s.st->partial, s.st->partial_elems, 2 * parts * cc));
+  float* part = s.st->partial;
+  const hipStream_t st = (hipStream_t)stream;
+  // dQw: the partials of X^T.hi and X^T.lo together, added into dQw once
+  TRY(xt_g_partials(s.st->handle, x, hi, R, C, parts, part));
+  TRY(xt_g_partials(s.st->handle, x, lo, R, C, parts, part + parts * cc));
+  TRY(reduce_into(part, 2 * parts, cc, dQw, false, st));
+  TRY(xt_g_partials(s.st->handle, x, dK, R, C, parts, part));
+  TRY(reduce_into(part, parts, cc, dKw, true, st));
+  TRY(xt_g_partials(s.st->handle, x, dV, R, C, parts, part));
+  return reduce_into(part, parts, cc, dVw, true, st);
 }
 
 }  // extern "C"
