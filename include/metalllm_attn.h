@@ -115,6 +115,65 @@ int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint1
 int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
                   uint16_t* dKw, uint16_t* dVw, const AttentionParams* p, metalllm_stream_t stream);
 
+/* elementwise.metal:19-28, model.h:692: out[i] = bf16(in[i]) for i < count (round to nearest
+ * even; NaN stays NaN). The reference's buffer order (in0 out1 count2). Allocates nothing.
+ * count == 0 is a no-op; otherwise both pointers non-NULL and 16-byte aligned. */
+int castFloatToBfloat(const float* in, uint16_t* out, uint32_t count, metalllm_stream_t stream);
+
+/* ---- Phase encoder (model.h:441-508 forward, :538-708 backward: one command buffer per phase) ----
+ * The attention sublayer's buffers, as model.h's BlockBuffers hold them (model.h:236-277). All
+ * device pointers, 16-byte aligned; shapes from AttentionParams as above (R = B*M rows, N = C
+ * features): activations [R, N], weights [N, N] [input][output], l and Dsum fp32 [B, NH, M]. */
+typedef struct metalllmSublayerBuffers {
+  const uint16_t* X;      /* bf16: the sublayer input (ln1 output, model.h:447)             */
+  const uint16_t* q_w;    /* bf16 weights                                                     */
+  const uint16_t* k_w;
+  const uint16_t* v_w;
+  const uint16_t* proj_w;
+  uint16_t* q;            /* bf16, written by the forward phase, read by the backward phase  */
+  uint16_t* k;
+  uint16_t* v;
+  uint16_t* attn_out;     /* bf16 attention output O                                          */
+  float* l;               /* fp32 logsumexp                                                    */
+  uint16_t* out;          /* bf16 sublayer output (forward phase)                              */
+  const uint16_t* dOut;   /* bf16 gradient at the sublayer output (model.h's dBranch, :622)    */
+  uint16_t* dAttn;        /* bf16 gradient at O (model.h's dZAttn, :633)                       */
+  float* Dsum;            /* fp32 computeD output                                               */
+  float* dQ;              /* fp32 accumulator                                                   */
+  uint16_t* dK;           /* bf16                                                               */
+  uint16_t* dV;
+  float* dX;              /* fp32 gradient at X (model.h's dXAttn)                              */
+  float* dQw;             /* fp32 [N, N]                                                        */
+  uint16_t* dKw;          /* bf16 [N, N]                                                        */
+  uint16_t* dVw;
+  uint16_t* dProjw;
+  uint16_t* dX_bf16;      /* optional (NULL: skipped): bf16(dX), model.h:692                   */
+} metalllmSublayerBuffers;
+
+typedef struct metalllmSublayerGraph metalllmSublayerGraph;
+
+/* Enqueues one phase of the sublayer on `stream`, in model.h's order.
+ *   phase 0 (model.h:444-483): computeQKV, flashAttentionForward, projForward.
+ *   phase 1 (model.h:549-555, 620-693): zero dQ, dX, dQw, dKw, dVw, dProjw; projBackwarddW,
+ *            projBackwarddX, computeD, flashAttentionBackward, computeGradDx, computeGradDw (one
+ *            two-term split of dQ serves both), and castFloatToBfloat(dX) when dX_bf16 is set.
+ * Validation: the GEMM rules and the attention rules above, every pointer the phase uses.
+ * Uses the device's shared rocBLAS handle and scratch like the GEMM entry points above. */
+int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
+                           metalllm_stream_t stream);
+
+/* Records the same phase once as a HIP graph (pointers and shapes fixed at creation) and returns
+ * it in *out; metalllmSublayerGraphLaunch replays it on `stream` with one launch, reading the
+ * buffers' current contents. A graph owns its rocBLAS handle, workspace and scratch (allocated
+ * here, freed by Destroy), so it never depends on memory other calls may reallocate. Replays of
+ * one graph must not overlap each other; Destroy only after the last replay completed. These
+ * three have no single counterpart in the reference (it re-encodes the command buffer each step,
+ * model.h:441,587). */
+int metalllmSublayerGraphCreate(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
+                                metalllmSublayerGraph** out);
+int metalllmSublayerGraphLaunch(metalllmSublayerGraph* g, metalllm_stream_t stream);
+int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g);
+
 /* Bench hook (no counterpart in the reference): launches one of the two kernels that
  * flashAttentionBackward runs, in this order, on `stream`: part 0 = dK/dV (key-block owners),
  * part 1 = dQ (query-block owners). flashAttentionBackward(args) is exactly part 0 followed by

@@ -24,7 +24,8 @@ ERRORS = {
 }
 EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
             "metalllmAttnErrorString", "metalllmAttnWorkMap", "computeQKV", "projForward", "projBackwarddW",
-            "projBackwarddX", "computeGradDx", "computeGradDw")
+            "projBackwarddX", "computeGradDx", "computeGradDw", "castFloatToBfloat", "metalllmSublayerEncode",
+            "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy")
 
 
 class AttentionParams(ctypes.Structure):

@@ -100,17 +100,31 @@ struct Session {
   }
 };
 
+// Where a sequence of GEMMs and helper kernels goes: the rocBLAS handle (already bound to
+// `stream`) and the stream. With `query` set, nothing is launched: rocBLAS calls only report the
+// device workspace they need (rocblas_start_device_memory_size_query is active on the handle).
+struct Ctx {
+  rocblas_handle h = nullptr;
+  hipStream_t stream = nullptr;
+  bool query = false;
+};
+
+bool blas_ok(const Ctx& c, rocblas_status s) {
+  return s == rocblas_status_success ||
+         (c.query && (s == rocblas_status_size_increased || s == rocblas_status_size_unchanged));
+}
+
 // Row-major C[M][N] = op(A)[M][K] . op(B)[K][N] + beta * C. op(A) = A stored [M][K] (lda) or, with
 // ta, A^T of A stored [K][M]; likewise op(B). rocBLAS is column-major: the row-major product is
 // computed as C^T = op(B)^T . op(A)^T on the same memory.
-int gemm_rm(rocblas_handle h, bool ta, bool tb, int M, int N, int K, const void* A, rocblas_datatype at, int lda,
+int gemm_rm(const Ctx& c, bool ta, bool tb, int M, int N, int K, const void* A, rocblas_datatype at, int lda,
             const void* B, rocblas_datatype bt, int ldb, float beta, void* C, rocblas_datatype ct, int ldc) {
   const float alpha = 1.0f;
   const rocblas_status s = rocblas_gemm_ex(
-      h, tb ? rocblas_operation_transpose : rocblas_operation_none, ta ? rocblas_operation_transpose : rocblas_operation_none,
+      c.h, tb ? rocblas_operation_transpose : rocblas_operation_none, ta ? rocblas_operation_transpose : rocblas_operation_none,
       N, M, K, &alpha, B, bt, ldb, A, at, lda, &beta, C, ct, ldc, C, ct, ldc, rocblas_datatype_f32_r,
       rocblas_gemm_algo_standard, 0, 0);
-  return s == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
+  return blas_ok(c, s) ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
 }
 
 constexpr rocblas_datatype BF = rocblas_datatype_bf16_r;
@@ -138,19 +152,14 @@ __global__ void __launch_bounds__(256) split_kernel(const float4* __restrict__ x
   }
 }
 
-// Splits dQ [R*C] into the device's split buffer on `stream`; returns hi (lo follows at + R*C).
-int split_dq(DeviceState& st, const float* dQ, size_t elems, hipStream_t stream, const uint16_t** hi,
-             const uint16_t** lo) {
-  const int rc = ensure(st.split, st.split_elems, 2 * elems);
-  if (rc) return rc;
+// Writes hi = bf16(dQ), lo = bf16(dQ - hi) into split[0 .. elems) and split[elems .. 2 elems).
+int split_dq(const Ctx& c, const float* dQ, size_t elems, uint16_t* split) {
+  if (c.query) return METALLLM_ATTN_OK;
   const size_t n4 = elems / 4;  // C is a multiple of 8 (validate_gemm)
   const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 65536);
-  hipLaunchKernelGGL(split_kernel, dim3(blocks), dim3(256), 0, stream, (const float4*)dQ, (uint2*)st.split,
-                     (uint2*)(st.split + elems), n4);
-  if (hipGetLastError() != hipSuccess) return METALLLM_ATTN_E_LAUNCH;
-  *hi = st.split;
-  *lo = st.split + elems;
-  return METALLLM_ATTN_OK;
+  hipLaunchKernelGGL(split_kernel, dim3(blocks), dim3(256), 0, c.stream, (const float4*)dQ, (uint2*)split,
+                     (uint2*)(split + elems), n4);
+  return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
 // Weight gradients W[k][n] += sum_r X[r][k] G[r][n] reduce over all R rows into a small C x C
@@ -164,15 +173,15 @@ int row_chunks(int R) {
   return 1;
 }
 
-int xt_g_partials(rocblas_handle h, const uint16_t* X, const uint16_t* G, int R, int C, int parts, float* out) {
+int xt_g_partials(const Ctx& c, const uint16_t* X, const uint16_t* G, int R, int C, int parts, float* out) {
   const float alpha = 1.0f, beta = 0.0f;
   const int Rs = R / parts;
   // row-major out_s[C][C] = X_s^T . G_s; column-major: out_s^T = G_s^T . X_s
   const rocblas_status st = rocblas_gemm_strided_batched_ex(
-      h, rocblas_operation_none, rocblas_operation_transpose, C, C, Rs, &alpha, G, BF, C, (rocblas_stride)Rs * C, X, BF,
-      C, (rocblas_stride)Rs * C, &beta, out, F32, C, (rocblas_stride)C * C, out, F32, C, (rocblas_stride)C * C, parts,
-      rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  return st == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
+      c.h, rocblas_operation_none, rocblas_operation_transpose, C, C, Rs, &alpha, G, BF, C, (rocblas_stride)Rs * C, X,
+      BF, C, (rocblas_stride)Rs * C, &beta, out, F32, C, (rocblas_stride)C * C, out, F32, C, (rocblas_stride)C * C,
+      parts, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  return blas_ok(c, st) ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
 }
 
 // dst[i] = round(dst[i] + sum_p part[p * n + i]) with the fp32 sum in p order; dst fp32 or bf16.
@@ -191,12 +200,13 @@ __global__ void __launch_bounds__(256) reduce_kernel(const float* __restrict__ p
   }
 }
 
-int reduce_into(const float* part, int nparts, size_t n, void* dst, bool bf16_dst, hipStream_t stream) {
+int reduce_into(const Ctx& c, const float* part, int nparts, size_t n, void* dst, bool bf16_dst) {
+  if (c.query) return METALLLM_ATTN_OK;
   const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
   if (bf16_dst)
-    hipLaunchKernelGGL(reduce_kernel<true>, dim3(blocks), dim3(256), 0, stream, part, nparts, n, dst);
+    hipLaunchKernelGGL(reduce_kernel<true>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst);
   else
-    hipLaunchKernelGGL(reduce_kernel<false>, dim3(blocks), dim3(256), 0, stream, part, nparts, n, dst);
+    hipLaunchKernelGGL(reduce_kernel<false>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst);
   return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
@@ -215,6 +225,79 @@ int reduce_into(const float* part, int nparts, size_t n, void* dst, bool bf16_ds
     }                                                             \
   } while (0)
 
+// ---- the reference kernels as sequences on a Ctx (R = B*M rows, C = N features) ----
+
+int op_qkv(const Ctx& c, const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w,
+           const uint16_t* k_w, const uint16_t* v_w, int R, int C) {
+  TRY(gemm_rm(c, false, false, R, C, C, X, BF, C, q_w, BF, C, 0.0f, q, BF, C));
+  TRY(gemm_rm(c, false, false, R, C, C, X, BF, C, k_w, BF, C, 0.0f, k, BF, C));
+  return gemm_rm(c, false, false, R, C, C, X, BF, C, v_w, BF, C, 0.0f, v, BF, C);
+}
+
+int op_proj_fwd(const Ctx& c, const uint16_t* attn_out, const uint16_t* proj_w, uint16_t* out, int R, int C) {
+  return gemm_rm(c, false, false, R, C, C, attn_out, BF, C, proj_w, BF, C, 0.0f, out, BF, C);
+}
+
+// partial: at least row_chunks(R) * C * C floats
+int op_proj_dw(const Ctx& c, const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, int R, int C,
+               float* partial) {
+  const int parts = row_chunks(R);
+  TRY(xt_g_partials(c, attn_out, dZ, R, C, parts, partial));
+  return reduce_into(c, partial, parts, (size_t)C * C, dProjw, true);
+}
+
+int op_proj_dx(const Ctx& c, const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, int R, int C) {
+  return gemm_rm(c, false, true, R, C, C, dZ, BF, C, proj_w, BF, C, 0.0f, dAttn, BF, C);
+}
+
+// hi, lo: the two-term bf16 split of dQ (split_dq)
+int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw,
+               const uint16_t* hi, const uint16_t* lo, const uint16_t* dK, const uint16_t* dV, int R, int C) {
+  TRY(gemm_rm(c, false, true, R, C, C, hi, BF, C, qw, BF, C, 1.0f, dX, F32, C));
+  TRY(gemm_rm(c, false, true, R, C, C, lo, BF, C, qw, BF, C, 1.0f, dX, F32, C));
+  TRY(gemm_rm(c, false, true, R, C, C, dK, BF, C, kw, BF, C, 1.0f, dX, F32, C));
+  return gemm_rm(c, false, true, R, C, C, dV, BF, C, vw, BF, C, 1.0f, dX, F32, C);
+}
+
+// partial: at least 2 * row_chunks(R) * C * C floats
+int op_grad_dw(const Ctx& c, const uint16_t* x, const uint16_t* hi, const uint16_t* lo, const uint16_t* dK,
+               const uint16_t* dV, float* dQw, uint16_t* dKw, uint16_t* dVw, int R, int C, float* part) {
+  const int parts = row_chunks(R);
+  const size_t cc = (size_t)C * C;
+  // dQw: the partials of X^T.hi and X^T.lo together, added into dQw once
+  TRY(xt_g_partials(c, x, hi, R, C, parts, part));
+  TRY(xt_g_partials(c, x, lo, R, C, parts, part + parts * cc));
+  TRY(reduce_into(c, part, 2 * parts, cc, dQw, false));
+  TRY(xt_g_partials(c, x, dK, R, C, parts, part));
+  TRY(reduce_into(c, part, parts, cc, dKw, true));
+  TRY(xt_g_partials(c, x, dV, R, C, parts, part));
+  return reduce_into(c, part, parts, cc, dVw, true);
+}
+
+// Zeroes n16 16-byte words (a fill kernel: no memset node when captured into a graph).
+__global__ void __launch_bounds__(256) zero_kernel(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+int zero_bytes(const Ctx& c, void* p, size_t bytes) {  // bytes a multiple of 16
+  if (c.query) return METALLLM_ATTN_OK;
+  const size_t n16 = bytes / 16;
+  const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 8192);
+  hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, c.stream, (uint4*)p, n16);
+  return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
+}
+
+// Public entry points: the device's handle and buffers, bound to the caller's stream.
+struct Public {
+  Session s;
+  Ctx c;
+  explicit Public(metalllm_stream_t stream) : s((hipStream_t)stream) {
+    c.h = s.st ? s.st->handle : nullptr;
+    c.stream = (hipStream_t)stream;
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -223,22 +306,18 @@ int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const u
                const uint16_t* v_w, const AttentionParams* p, metalllm_stream_t stream) {
   TRY(validate_gemm(p));
   CHECK_PTRS(X, q, k, v, q_w, k_w, v_w);
-  const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  TRY(gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, q_w, BF, C, 0.0f, q, BF, C));
-  TRY(gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, k_w, BF, C, 0.0f, k, BF, C));
-  return gemm_rm(s.st->handle, false, false, R, C, C, X, BF, C, v_w, BF, C, 0.0f, v, BF, C);
+  Public u(stream);
+  TRY(u.s.rc);
+  return op_qkv(u.c, X, q, k, v, q_w, k_w, v_w, (int)(p->B * p->M), (int)p->N);
 }
 
 int projForward(const uint16_t* attn_out, const uint16_t* proj_w, uint16_t* out, const AttentionParams* p,
                 metalllm_stream_t stream) {
   TRY(validate_gemm(p));
   CHECK_PTRS(attn_out, proj_w, out);
-  const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  return gemm_rm(s.st->handle, false, false, R, C, C, attn_out, BF, C, proj_w, BF, C, 0.0f, out, BF, C);
+  Public u(stream);
+  TRY(u.s.rc);
+  return op_proj_fwd(u.c, attn_out, proj_w, out, (int)(p->B * p->M), (int)p->N);
 }
 
 int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, const AttentionParams* p,
@@ -246,22 +325,19 @@ int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProj
   TRY(validate_gemm(p));
   CHECK_PTRS(attn_out, dZ, dProjw);
   const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  const int parts = row_chunks(R);
-  TRY(ensure(s.st->partial, s.st->partial_elems, (size_t)parts * C * C));
-  TRY(xt_g_partials(s.st->handle, attn_out, dZ, R, C, parts, s.st->partial));
-  return reduce_into(s.st->partial, parts, (size_t)C * C, dProjw, true, (hipStream_t)stream);
+  Public u(stream);
+  TRY(u.s.rc);
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, (size_t)row_chunks(R) * C * C));
+  return op_proj_dw(u.c, attn_out, dZ, dProjw, R, C, u.s.st->partial);
 }
 
 int projBackwarddX(const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, const AttentionParams* p,
                    metalllm_stream_t stream) {
   TRY(validate_gemm(p));
   CHECK_PTRS(dZ, proj_w, dAttn);
-  const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  return gemm_rm(s.st->handle, false, true, R, C, C, dZ, BF, C, proj_w, BF, C, 0.0f, dAttn, BF, C);
+  Public u(stream);
+  TRY(u.s.rc);
+  return op_proj_dx(u.c, dZ, proj_w, dAttn, (int)(p->B * p->M), (int)p->N);
 }
 
 int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
@@ -269,14 +345,12 @@ int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint1
   TRY(validate_gemm(p));
   CHECK_PTRS(dX, qw, kw, vw, dQ, dK, dV);
   const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  const uint16_t *hi = nullptr, *lo = nullptr;
-  TRY(split_dq(*s.st, dQ, (size_t)R * C, (hipStream_t)stream, &hi, &lo));
-  TRY(gemm_rm(s.st->handle, false, true, R, C, C, hi, BF, C, qw, BF, C, 1.0f, dX, F32, C));
-  TRY(gemm_rm(s.st->handle, false, true, R, C, C, lo, BF, C, qw, BF, C, 1.0f, dX, F32, C));
-  TRY(gemm_rm(s.st->handle, false, true, R, C, C, dK, BF, C, kw, BF, C, 1.0f, dX, F32, C));
-  return gemm_rm(s.st->handle, false, true, R, C, C, dV, BF, C, vw, BF, C, 1.0f, dX, F32, C);
+  const size_t e = (size_t)R * C;
+  Public u(stream);
+  TRY(u.s.rc);
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e));
+  TRY(split_dq(u.c, dQ, e, u.s.st->split));
+  return op_grad_dx(u.c, dX, qw, kw, vw, u.s.st->split, u.s.st->split + e, dK, dV, R, C);
 }
 
 int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
@@ -284,23 +358,175 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
   TRY(validate_gemm(p));
   CHECK_PTRS(x, dQ, dK, dV, dQw, dKw, dVw);
   const int R = (int)(p->B * p->M), C = (int)p->N;
-  Session s((hipStream_t)stream);
-  TRY(s.rc);
-  const uint16_t *hi = nullptr, *lo = nullptr;
-  TRY(split_dq(*s.st, dQ, (size_t)R * C, (hipStream_t)stream, &hi, &lo));
-  const int parts = row_chunks(R);
-  const size_t cc = (size_t)C * C;
-  TRY(ensure(s.st->partial, s.st->partial_elems, 2 * parts * cc));
-  float* part = s.st->partial;
-  const hipStream_t st = (hipStream_t)stream;
-  // dQw: the partials of X^T.hi and X^T.lo together, added into dQw once
-  TRY(xt_g_partials(s.st->handle, x, hi, R, C, parts, part));
-  TRY(xt_g_partials(s.st->handle, x, lo, R, C, parts, part + parts * cc));
-  TRY(reduce_into(part, 2 * parts, cc, dQw, false, st));
-  TRY(xt_g_partials(s.st->handle, x, dK, R, C, parts, part));
-  TRY(reduce_into(part, parts, cc, dKw, true, st));
-  TRY(xt_g_partials(s.st->handle, x, dV, R, C, parts, part));
-  return reduce_into(part, parts, cc, dVw, true, st);
+  const size_t e = (size_t)R * C;
+  Public u(stream);
+  TRY(u.s.rc);
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C));
+  TRY(split_dq(u.c, dQ, e, u.s.st->split));
+  return op_grad_dw(u.c, x, u.s.st->split, u.s.st->split + e, dK, dV, dQw, dKw, dVw, R, C, u.s.st->partial);
+}
+
+}  // extern "C"
+
+// ---- Phase encoder ----
+// model.h encodes each phase of a training step into one command buffer (forward :441-508,
+// backward :587-708) and commits it once (commitWait, :358-366); the buffers are allocated once
+// in the constructor (:236-277), so the same dispatches run on the same buffers every step. The
+// MI355X form is a HIP graph per phase of the attention sublayer: the launches are recorded once
+// on a private stream with the pointers and shapes baked in, and replayed with one launch. Each
+// graph owns its rocBLAS handle, that handle's workspace (sized by a rocBLAS size query before
+// capture) and its scratch (dQ split, weight-gradient partials), so nothing a replay touches is
+// ever reallocated by other calls.
+struct metalllmSublayerGraph {
+  int phase = 0;
+  rocblas_handle h = nullptr;
+  void* workspace = nullptr;
+  uint16_t* split = nullptr;
+  float* partial = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int check_phase(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p) {
+  if (!b || !p) return METALLLM_ATTN_E_NULL;
+  if (phase != 0 && phase != 1) return METALLLM_ATTN_E_LAYOUT;
+  TRY(validate_gemm(p));
+  if (p->M % 64) return METALLLM_ATTN_E_SEQLEN;
+  if (p->D != 64 && p->D != 128) return METALLLM_ATTN_E_HEADDIM;
+  if (phase == 0) {
+    CHECK_PTRS(b->X, b->q_w, b->k_w, b->v_w, b->proj_w, b->q, b->k, b->v, b->attn_out, b->l, b->out);
+  } else {
+    CHECK_PTRS(b->X, b->q_w, b->k_w, b->v_w, b->proj_w, b->q, b->k, b->v, b->attn_out, b->l, b->dOut, b->dAttn,
+               b->Dsum, b->dQ, b->dK, b->dV, b->dX, b->dQw, b->dKw, b->dVw, b->dProjw);
+    if (b->dX_bf16 && !aligned16(b->dX_bf16)) return METALLLM_ATTN_E_ALIGN;
+  }
+  return METALLLM_ATTN_OK;
+}
+
+// The launch sequence of one phase (model.h:444-483 forward, :549-555 and :620-693 backward).
+int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const AttentionParams* p, uint16_t* split,
+           float* partial) {
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  const size_t e = (size_t)R * C;
+  const metalllm_stream_t s = (metalllm_stream_t)c.stream;
+  if (phase == 0) {
+    TRY(op_qkv(c, b->X, b->q, b->k, b->v, b->q_w, b->k_w, b->v_w, R, C));
+    if (!c.query) TRY(flashAttentionForward(b->q, b->k, b->v, b->attn_out, b->l, p, s));
+    return op_proj_fwd(c, b->attn_out, b->proj_w, b->out, R, C);
+  }
+  // model.h:549-555 zeroes the accumulated gradients before the pass (dK and dV are written in full)
+  TRY(zero_bytes(c, b->dQ, e * 4));
+  TRY(zero_bytes(c, b->dX, e * 4));
+  TRY(zero_bytes(c, b->dQw, (size_t)C * C * 4));
+  TRY(zero_bytes(c, b->dKw, (size_t)C * C * 2));
+  TRY(zero_bytes(c, b->dVw, (size_t)C * C * 2));
+  TRY(zero_bytes(c, b->dProjw, (size_t)C * C * 2));
+  TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial));
+  TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
+  if (!c.query) {
+    TRY(computeD(b->dAttn, b->attn_out, b->Dsum, p, s));
+    TRY(flashAttentionBackward(b->dAttn, b->Dsum, b->l, b->q, b->k, b->v, b->dQ, b->dK, b->dV, p, s));
+  }
+  TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
+  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, split, split + e, b->dK, b->dV, R, C));
+  TRY(op_grad_dw(c, b->X, split, split + e, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
+  if (b->dX_bf16 && !c.query) TRY(castFloatToBfloat(b->dX, b->dX_bf16, (uint32_t)e, s));
+  return METALLLM_ATTN_OK;
+}
+
+int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, const AttentionParams* p) {
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  if (rocblas_create_handle(&g->h) != rocblas_status_success) {
+    g->h = nullptr;
+    return METALLLM_ATTN_E_LIBRARY;
+  }
+  if (g->phase == 1) {
+    if (hipMalloc((void**)&g->split, 2 * (size_t)R * C * sizeof(uint16_t)) != hipSuccess) g->split = nullptr;
+    if (hipMalloc((void**)&g->partial, 2 * (size_t)row_chunks(R) * C * C * sizeof(float)) != hipSuccess)
+      g->partial = nullptr;
+    if (!g->split || !g->partial) return METALLLM_ATTN_E_LIBRARY;
+  }
+  // the workspace the phase's rocBLAS calls need, owned by the graph
+  size_t ws = 0;
+  if (rocblas_start_device_memory_size_query(g->h) != rocblas_status_success) return METALLLM_ATTN_E_LIBRARY;
+  Ctx q;
+  q.h = g->h;
+  q.query = true;
+  const int qrc = encode(q, g->phase, b, p, g->split, g->partial);
+  if (rocblas_stop_device_memory_size_query(g->h, &ws) != rocblas_status_success || qrc) return METALLLM_ATTN_E_LIBRARY;
+  if (ws && hipMalloc(&g->workspace, ws) != hipSuccess) {
+    g->workspace = nullptr;
+    return METALLLM_ATTN_E_LIBRARY;
+  }
+  if (rocblas_set_workspace(g->h, g->workspace, ws) != rocblas_status_success) return METALLLM_ATTN_E_LIBRARY;
+  hipStream_t cap = nullptr;
+  if (hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
+  int rc = rocblas_set_stream(g->h, cap) == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
+  if (!rc && hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = METALLLM_ATTN_E_LIBRARY;
+  else if (!rc) {
+    Ctx c;
+    c.h = g->h;
+    c.stream = cap;
+    rc = encode(c, g->phase, b, p, g->split, g->partial);
+    const hipError_t e = hipStreamEndCapture(cap, &g->graph);  // always ends the capture
+    if (!rc && e != hipSuccess) rc = METALLLM_ATTN_E_LIBRARY;
+  }
+  if (!rc && hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0) != hipSuccess) rc = METALLLM_ATTN_E_LIBRARY;
+  (void)hipStreamDestroy(cap);
+  return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
+                           metalllm_stream_t stream) {
+  TRY(check_phase(phase, b, p));
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  Public u(stream);
+  TRY(u.s.rc);
+  if (phase == 1) {
+    TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C));
+    TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C));
+  }
+  return encode(u.c, phase, b, p, u.s.st->split, u.s.st->partial);
+}
+
+int metalllmSublayerGraphCreate(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
+                                metalllmSublayerGraph** out) {
+  if (!out) return METALLLM_ATTN_E_NULL;
+  *out = nullptr;
+  TRY(check_phase(phase, b, p));
+  metalllmSublayerGraph* g = new metalllmSublayerGraph();
+  g->phase = phase;
+  const int rc = build_graph(g, b, p);
+  if (rc) {
+    metalllmSublayerGraphDestroy(g);
+    return rc;
+  }
+  *out = g;
+  return METALLLM_ATTN_OK;
+}
+
+int metalllmSublayerGraphLaunch(metalllmSublayerGraph* g, metalllm_stream_t stream) {
+  if (!g || !g->exec) return METALLLM_ATTN_E_NULL;
+  return hipGraphLaunch(g->exec, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
+}
+
+int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g) {
+  if (!g) return METALLLM_ATTN_OK;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  if (g->h) (void)rocblas_destroy_handle(g->h);
+  if (g->workspace) (void)hipFree(g->workspace);
+  if (g->split) (void)hipFree(g->split);
+  if (g->partial) (void)hipFree(g->partial);
+  delete g;
+  return METALLLM_ATTN_OK;
 }
 
 }  // extern "C"

@@ -1,7 +1,10 @@
 """Host side of the attention sublayer around the attention core: ctypes bindings of the six GEMM
 entry points of libmetalllm_attn.so (computeQKV, projForward, projBackwarddW, projBackwarddX,
-computeGradDx, computeGradDw; /root/reference/attention.metal:19-53, 301-455) and the sublayer's
-forward and backward chains in the order /root/reference/model.h:446-482 and :621-690 encode them.
+computeGradDx, computeGradDw; /root/reference/attention.metal:19-53, 301-455), of the dX handoff
+castFloatToBfloat (elementwise.metal:19-28, model.h:692), and of the phase encoder: the sublayer's
+forward and backward chains in the order /root/reference/model.h:446-482 and :621-693 encode them,
+enqueued eagerly (metalllmSublayerEncode) or recorded once as a HIP graph per phase and replayed
+(metalllmSublayerGraph*), the MI355X form of model.h's one command buffer per phase.
 
 Tensors are torch tensors on the GPU, contiguous: activations [B, T, C] (or [R, C]) with C = H*D,
 weights [C, C] indexed [input feature][output feature]. No CPU fallback: every product runs on
@@ -29,10 +32,26 @@ def _L():
         L.projBackwarddX.argtypes = [vp] * 3 + [pp, vp]
         L.computeGradDx.argtypes = [vp] * 7 + [pp, vp]
         L.computeGradDw.argtypes = [vp] * 7 + [pp, vp]
-        for f in (L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw):
+        L.castFloatToBfloat.argtypes = [vp, vp, ctypes.c_uint32, vp]
+        bp = ctypes.POINTER(SublayerBuffers)
+        L.metalllmSublayerEncode.argtypes = [ctypes.c_int, bp, pp, vp]
+        L.metalllmSublayerGraphCreate.argtypes = [ctypes.c_int, bp, pp, ctypes.POINTER(vp)]
+        L.metalllmSublayerGraphLaunch.argtypes = [vp, vp]
+        L.metalllmSublayerGraphDestroy.argtypes = [vp]
+        for f in (L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw,
+                  L.castFloatToBfloat, L.metalllmSublayerEncode, L.metalllmSublayerGraphCreate,
+                  L.metalllmSublayerGraphLaunch, L.metalllmSublayerGraphDestroy):
             f.restype = ctypes.c_int
         _BOUND = True
     return L
+
+
+class SublayerBuffers(ctypes.Structure):
+    """metalllmSublayerBuffers: the sublayer's device buffers (model.h:236-277), field order as in
+    include/metalllm_attn.h."""
+    FIELDS = ("X", "q_w", "k_w", "v_w", "proj_w", "q", "k", "v", "attn_out", "l", "out", "dOut", "dAttn", "Dsum", "dQ",
+              "dK", "dV", "dX", "dQw", "dKw", "dVw", "dProjw", "dX_bf16")
+    _fields_ = [(n, ctypes.c_void_p) for n in FIELDS]
 
 
 def params_of(x, H: int) -> AttentionParams:
@@ -79,6 +98,44 @@ def computeGradDw(x, dQ, dK, dV, dQw, dKw, dVw, p: AttentionParams, stream=None)
                               ctypes.byref(p), _stream(stream)), "computeGradDw")
 
 
+def castFloatToBfloat(inp, out, count=None, stream=None):
+    """elementwise.metal:19-28: out[i] = bf16(in[i]) (round to nearest even) for i < count."""
+    n = inp.numel() if count is None else count
+    _check(_L().castFloatToBfloat(_ptr(inp), _ptr(out), n, _stream(stream)), "castFloatToBfloat")
+
+
+def encode_phase(phase: int, bufs: SublayerBuffers, p: AttentionParams, stream=None):
+    """metalllmSublayerEncode: enqueue phase 0 (forward) or 1 (backward) eagerly."""
+    _check(_L().metalllmSublayerEncode(phase, ctypes.byref(bufs), ctypes.byref(p), _stream(stream)),
+           "metalllmSublayerEncode")
+
+
+class PhaseGraph:
+    """One phase recorded as a HIP graph (metalllmSublayerGraphCreate); launch() replays it."""
+
+    def __init__(self, phase: int, bufs: SublayerBuffers, p: AttentionParams):
+        self._g = ctypes.c_void_p()
+        self._L = _L()
+        _check(self._L.metalllmSublayerGraphCreate(phase, ctypes.byref(bufs), ctypes.byref(p), ctypes.byref(self._g)),
+               "metalllmSublayerGraphCreate")
+
+    def launch(self, stream=None):
+        _check(self._L.metalllmSublayerGraphLaunch(self._g, _stream(stream)), "metalllmSublayerGraphLaunch")
+
+    def close(self):
+        if self._g:
+            import torch
+            torch.cuda.synchronize()
+            _check(self._L.metalllmSublayerGraphDestroy(self._g), "metalllmSublayerGraphDestroy")
+            self._g = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Sublayer:
     """Buffers and launch sequence of one attention sublayer (pre-LN block, without the layernorm
     and residual glue), mirroring model.h: forward computeQKV -> flashAttentionForward ->
@@ -104,7 +161,43 @@ class Sublayer:
         self.dWk = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
         self.dWv = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
         self.dWp = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
+        self.dOut = bf()      # the phase encoder's input gradient buffer (model.h's dBranch)
+        self.dXb = bf()       # bf16(dX), the handoff to the layernorm backward (model.h:692)
         self.D = D
+        self.graphs = None
+
+    def buffers(self, cast: bool = True) -> SublayerBuffers:
+        """The struct of device pointers; cast=False leaves dX_bf16 NULL (no dX handoff)."""
+        b = SublayerBuffers()
+        t = dict(X=self.X, q_w=self.Wq, k_w=self.Wk, v_w=self.Wv, proj_w=self.Wp, q=self.q, k=self.k, v=self.v,
+                 attn_out=self.o, l=self.lse, out=self.out, dOut=self.dOut, dAttn=self.dO, Dsum=self.Dv, dQ=self.dQ,
+                 dK=self.dK, dV=self.dV, dX=self.dX, dQw=self.dWq, dKw=self.dWk, dVw=self.dWv, dProjw=self.dWp,
+                 dX_bf16=self.dXb)
+        if not cast:
+            t["dX_bf16"] = None
+        for n in SublayerBuffers.FIELDS:
+            setattr(b, n, _ptr(t[n]).value if t[n] is not None else None)
+        return b
+
+    def encode(self, phase: int, stream=None):
+        """One phase through the native encoder (eager launches). Phase 1 reads self.dOut and
+        zeroes the accumulated gradients first, as model.h:549-555 does."""
+        encode_phase(phase, self.buffers(), self.p, stream)
+
+    def capture(self):
+        """Records both phases as HIP graphs on the current buffers."""
+        b = self.buffers()
+        self.graphs = (PhaseGraph(0, b, self.p), PhaseGraph(1, b, self.p))
+        return self.graphs
+
+    def replay(self, phase: int, stream=None):
+        self.graphs[phase].launch(stream)
+
+    def close(self):
+        if self.graphs:
+            for g in self.graphs:
+                g.close()
+            self.graphs = None
 
     def forward(self, stream=None):
         p = self.p

@@ -172,6 +172,16 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     return u.astype(np.uint16)
 
 
+def castFloatToBfloat(x: np.ndarray) -> np.ndarray:
+    """elementwise.metal:19-28 (used at model.h:692): out[i] = bfloat(in[i]). Metal's float -> bfloat
+    conversion rounds to nearest even; overflow rounds to infinity; a NaN stays a quiet NaN of the
+    same sign (payload's top bits kept)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    r = np.where((u & 0x7FFFFFFF) > 0x7F800000, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
 # ---- sublayer GEMMs (gemm_oracle.cpp): row-major, R = B*T rows, C = NH*D features ----
 T_BF16, T_F32 = 0, 1
 _GEMM_BOUND = False

@@ -100,3 +100,66 @@ def test_sublayer_gemms_validate_before_device(name):
     assert f(*([ok] * (n - 1)), None, ctypes.byref(p), None) == -1
     assert f(*([ok] * (n - 1)), ctypes.c_void_p((1 << 20) + 4), ctypes.byref(p), None) == -6
     assert f(*([ok] * n), None, None) == -1
+
+
+def test_cast_validates_before_device():
+    lib = M.library()
+    f = lib.castFloatToBfloat
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
+    ok = ctypes.c_void_p(1 << 20)
+    assert f(None, None, 0, None) == 0  # count 0: nothing to do
+    assert f(None, ok, 16, None) == -1
+    assert f(ok, None, 16, None) == -1
+    assert f(ctypes.c_void_p((1 << 20) + 8), ok, 16, None) == -6
+    assert f(ok, ctypes.c_void_p((1 << 20) + 2), 16, None) == -6
+
+
+def test_sublayer_buffers_struct_matches_header():
+    """The ctypes struct's field order is the header's."""
+    from metalllm_amd.sublayer import SublayerBuffers
+    text = open(os.path.join(ROOT, "include", "metalllm_attn.h")).read()
+    body = text[text.index("typedef struct metalllmSublayerBuffers {"):text.index("} metalllmSublayerBuffers;")]
+    names = re.findall(r"\*\s*(\w+);", body)
+    assert tuple(names) == SublayerBuffers.FIELDS
+
+
+@pytest.mark.parametrize("entry", ["metalllmSublayerEncode", "metalllmSublayerGraphCreate"])
+def test_phase_encoder_validates_before_device(entry):
+    """Both phases reject bad phases, shapes (the GEMM rules and the attention rules: M % 64,
+    D in {64, 128}), NULL and misaligned buffers without touching the device."""
+    from metalllm_amd.sublayer import SublayerBuffers, _L
+    lib = _L()
+    f = getattr(lib, entry)
+    out = ctypes.c_void_p()
+    last = ctypes.byref(out) if entry.endswith("Create") else None
+
+    def call(phase, b, p):
+        return f(phase, ctypes.byref(b) if b is not None else None, ctypes.byref(p) if p is not None else None, last)
+
+    full = SublayerBuffers(*[(1 << 20) + 256 * i for i in range(len(SublayerBuffers.FIELDS))])
+    good = dict(M=256, N=384, D=64, NH=6, B=1)
+    P = lambda **c: AttentionParams(*[{**good, **c}[k] for k in ("M", "N", "D", "NH", "B")])
+    for phase in (0, 1):
+        assert call(phase, None, P()) == -1
+        assert call(phase, full, None) == -1
+        for change, code in ((dict(M=0), -2), (dict(M=96), -2), (dict(D=96, N=576), -3), (dict(D=32, N=192), -3),
+                             (dict(N=383), -4), (dict(B=0), -4), (dict(B=1 << 12, M=1 << 16), -5)):
+            assert call(phase, full, P(**change)) == code, (phase, change)
+    assert call(2, full, P()) == -4
+    assert call(-1, full, P()) == -4
+    # a NULL or misaligned buffer the phase uses
+    for name, phases in (("X", (0, 1)), ("out", (0,)), ("dOut", (1,)), ("dProjw", (1,)), ("l", (0, 1))):
+        for phase in phases:
+            b = SublayerBuffers(*[getattr(full, n) for n in SublayerBuffers.FIELDS])
+            setattr(b, name, None)
+            assert call(phase, b, P()) == -1, (name, phase)
+            setattr(b, name, getattr(full, name) + 4)
+            assert call(phase, b, P()) == -6, (name, phase)
+    b = SublayerBuffers(*[getattr(full, n) for n in SublayerBuffers.FIELDS])
+    b.dX_bf16 = full.dX_bf16 + 2  # optional, but aligned when given
+    assert call(1, b, P()) == -6
+    if entry.endswith("Create"):
+        assert lib.metalllmSublayerGraphCreate(0, ctypes.byref(full), ctypes.byref(P()), None) == -1
+        assert out.value is None
+        assert lib.metalllmSublayerGraphLaunch(None, None) == -1
+        assert lib.metalllmSublayerGraphDestroy(None) == 0

@@ -1,0 +1,116 @@
+"""GPU tests of the dX handoff (castFloatToBfloat, elementwise.metal:19-28) and of the phase
+encoder (metalllmSublayerEncode / metalllmSublayerGraph*: model.h's forward and backward
+command buffers, :441-508 and :538-708, as launch sequences and HIP graphs).
+
+Bars: the cast is bit-exact against the oracle. The encoder runs the same kernels on the same
+inputs as the per-call chain (whose stages test_gpu_sublayer.py checks against the oracle), so its
+results must be bit-identical to that chain; every kernel on the path is deterministic (dQ gets
+one fp32 add per element into a zeroed buffer). Graph replays must be bit-identical to the eager
+encoder on the same inputs, replay after replay, with eager work and new inputs in between.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.attn_case import to_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+OUTPUTS = ("q", "k", "v", "o", "lse", "out", "dO", "Dv", "dQ", "dK", "dV", "dX", "dWq", "dWk", "dWv", "dWp")
+
+
+@pytest.fixture(scope="module")
+def S():
+    import metalllm_amd.sublayer as S
+    return S
+
+
+def test_cast_float_to_bfloat(gpu, S):
+    import torch
+    rng = np.random.default_rng(11)
+    n = 1_000_003  # not a multiple of 4: the tail path
+    x = rng.standard_normal(n).astype(np.float32) * 10
+    x[:8] = np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF, 0xFF800000, 0x80000000, 0x00018000, 0x7F800001,
+                      0xFFC12345], dtype=np.uint32).view(np.float32)
+    x[-3:] = np.array([0x3F7FFFFF, 0x3F808001, 0x00000001], dtype=np.uint32).view(np.float32)
+    tin = to_gpu(x, gpu)
+    out = torch.full((n,), -1, dtype=torch.int16, device=gpu).view(torch.bfloat16)
+    S.castFloatToBfloat(tin, out)
+    torch.cuda.synchronize()
+    got, ref = to_np(out), O.castFloatToBfloat(x)
+    print(f"cast: {int((got != ref).sum())} of {n} differ")
+    assert np.array_equal(got, ref)
+    # a shorter count leaves the rest untouched
+    out2 = torch.full((16,), 0x1234, dtype=torch.int16, device=gpu).view(torch.bfloat16)
+    S.castFloatToBfloat(tin[:16], out2, count=7)
+    torch.cuda.synchronize()
+    g2 = to_np(out2)
+    assert np.array_equal(g2[:7], ref[:7]) and (g2[7:] == 0x1234).all()
+
+
+def _sublayer(S, gpu, B, T, H, C, seed):
+    rng = np.random.default_rng(seed)
+    bf = lambda shape, sc=1.0: to_gpu(O.f32_to_bf16((rng.standard_normal(shape) * sc).astype(np.float32)), gpu)
+    X = bf((B, T, C))
+    Ws = [bf((C, C), 0.02) for _ in range(4)]
+    return S.Sublayer(X, *Ws, H=H), bf((B, T, C))
+
+
+def _snapshot(sub):
+    import torch
+    torch.cuda.synchronize()
+    return {n: to_np(getattr(sub, n)).copy() for n in OUTPUTS + ("dXb",)}
+
+
+def test_encoder_matches_per_call_chain(gpu, S):
+    """metalllmSublayerEncode(0), (1) == the chain of public entry points (model.h order), bit for
+    bit, and its dX_bf16 is castFloatToBfloat(dX)."""
+    import torch
+    B, T, H, C = 2, 512, 12, 768
+    a, dOut = _sublayer(S, gpu, B, T, H, C, 21)
+    b = S.Sublayer(a.X, a.Wq, a.Wk, a.Wv, a.Wp, H=H)
+    # per-call chain on a
+    a.zero_grads()
+    a.forward()
+    a.backward(dOut)
+    # encoder on b; gradients start dirty: phase 1 must zero them itself
+    for t in (b.dQ, b.dX, b.dWq, b.dWk, b.dWv, b.dWp):
+        t.fill_(3.0)
+    b.dOut.copy_(dOut)
+    b.encode(0)
+    b.encode(1)
+    ra, rb = _snapshot(a), _snapshot(b)
+    for n in OUTPUTS:
+        same = np.array_equal(ra[n], rb[n])
+        print(f"{n}: {'identical' if same else 'DIFFERENT'}")
+        assert same, n
+    assert np.array_equal(rb["dXb"], O.castFloatToBfloat(rb["dX"]))
+
+
+def test_graph_replays_match_encoder(gpu, S):
+    """Both phases recorded as graphs replay bit-identically to the eager encoder on new inputs,
+    three times, with eager work and synchronisations between the replays; one config-4 shape
+    (D = 64) and one D = 128 shape."""
+    import torch
+    for (B, T, H, C) in ((1, 2048, 12, 768), (2, 256, 4, 512)):
+        g, _ = _sublayer(S, gpu, B, T, H, C, 31)
+        e = S.Sublayer(g.X.clone(), g.Wq, g.Wk, g.Wv, g.Wp, H=H)
+        g.capture()
+        rng = np.random.default_rng(32)
+        for it in range(3):
+            x = to_gpu(O.f32_to_bf16(rng.standard_normal((B, T, C)).astype(np.float32)), gpu)
+            d = to_gpu(O.f32_to_bf16(rng.standard_normal((B, T, C)).astype(np.float32)), gpu)
+            g.X.copy_(x)
+            g.dOut.copy_(d)
+            e.X.copy_(x)
+            e.dOut.copy_(d)
+            g.replay(0)
+            g.replay(1)
+            torch.cuda.synchronize()
+            e.encode(0)  # eager work between replays
+            e.encode(1)
+            rg, re = _snapshot(g), _snapshot(e)
+            for n in OUTPUTS + ("dXb",):
+                assert np.array_equal(rg[n], re[n]), (B, T, H, C, it, n)
+            print(f"shape {(B, T, H, C)} replay {it}: identical to the encoder")
+        g.close()
