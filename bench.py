@@ -3,18 +3,22 @@ flashAttentionBackward) on one MI355X, through the C ABI.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
 
-One step = dQ zeroing + flashAttentionForward + computeD + flashAttentionBackward over one batch of
-synthetic bf16 inputs already resident in HBM (the reference's per-layer sequence, model.h:459-473,
-549-551, 639-665). Prints ONE JSON line. FLOPs use the causal FlashAttention convention (half of
-dense): fwd 2*B*H*T^2*D, bwd 5*B*H*T^2*D, step 7*B*H*T^2*D.
+One step = flashAttentionForward + computeD + the backward over one batch of synthetic bf16 inputs
+already resident in HBM (the reference's per-layer sequence, model.h:459-473, 639-665). The
+backward is flashAttentionBackwardWorkspace (dK/dV kernel storing dS into a device workspace, then
+dQ = dS.K; workspace allocated once, outside the timed region, like the other buffers); the
+recomputing flashAttentionBackward is timed beside it ("bwd_recompute"). Prints ONE JSON line.
+FLOPs use the causal FlashAttention convention (half of dense): fwd 2*B*H*T^2*D, bwd
+5*B*H*T^2*D, step 7*B*H*T^2*D.
 
-The roofline object describes the dominant kernel, the dK/dV kernel of flashAttentionBackward
-(mla::bwd_kernel; flashAttentionBackward launches it and then the dQ kernel, and the bench launches
-the two through metalllmAttnBackwardPart so that each has its own events): its algorithmic FLOPs
-per launch (4 causal products: S, dP, dV, dK) over its average launch time measured with HIP events
-on the launch stream, against MI355X dense bf16 matrix peak. cpu_baseline times the CPU oracle (the scalar C++ transcription
-of the reference math, oracle/attn_oracle.cpp) on a bounded sample of the same workload on this
-host's cores.
+The roofline object describes the dominant kernel, the dK/dV kernel (mla::bwd_kernel with the dS
+store; the bench launches the backward's two kernels through metalllmAttnBackwardPart so that
+each has its own events): its algorithmic FLOPs per launch (4 causal products: S, dP, dV, dK) over
+its average launch time measured with HIP events on the launch stream, against MI355X dense bf16
+matrix peak. roofline_dq does the same for the HBM-bound dQ kernel (bytes of dS, K and dQ per
+launch against 8 TB/s). cpu_baseline times the CPU oracle (the scalar C++ transcription of the
+reference math, oracle/attn_oracle.cpp) on a bounded sample of the same workload on this host's
+cores.
 """
 from __future__ import annotations
 
@@ -43,9 +47,9 @@ def flops(B, H, T, D):
     return 2.0 * base, 5.0 * base
 
 
-def traffic_from_profiles(cfg_id):
-    """HBM bytes per dK/dV-kernel launch measured by rocprofv3 --pmc, if a summary was committed."""
-    path = os.path.join(ROOT, "profiles", f"bwd_dkdv_traffic_config{cfg_id}.json")
+def traffic_from_profiles(cfg_id, kernel="bwd_dkdv"):
+    """HBM bytes per launch of a kernel measured by rocprofv3 --pmc, if a summary was committed."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic_config{cfg_id}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -221,13 +225,15 @@ def main():
     dQ = torch.empty(shape, dtype=torch.float32, device=dev)
     dK = torch.empty_like(q)
     dV = torch.empty_like(q)
+    ws_bytes = M.workspace_bytes(B, T, H, D)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     p = M.AttentionParams.of(B, T, H, D)
 
-    # flashAttentionBackward == part 0 (dK/dV kernel) then part 1 (dQ kernel) on the same stream;
-    # the bench launches the parts itself so that each kernel is timed by its own events
-    def step(ev=None):
-        dQ.zero_()
+    # flashAttentionBackwardWorkspace == part 2 (dK/dV kernel + dS store) then part 3 (dQ from dS);
+    # flashAttentionBackward == part 0 then part 1. The bench launches the parts itself so that
+    # each kernel is timed by its own events.
+    def step(ev=None, parts=(2, 3)):
         if ev is not None:
             ev[0].record(stream)
         M.flashAttentionForward(q, k, v, out, lse, stream, p)
@@ -236,12 +242,20 @@ def main():
         M.computeD(dO, out, Dv, stream, p)
         if ev is not None:
             ev[2].record(stream)
-        M.backward_part(0, dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
+        M.backward_part(parts[0], dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p, workspace=ws)
         if ev is not None:
             ev[3].record(stream)
-        M.backward_part(1, dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p)
+        M.backward_part(parts[1], dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p, workspace=ws)
         if ev is not None:
             ev[4].record(stream)
+
+    # the recomputing backward, for comparison (its own warmup and events)
+    for _ in range(2):
+        step(parts=(0, 1))
+    rc_events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(max(3, args.steps // 4))]
+    for e in rc_events:
+        step(e, parts=(0, 1))
+    torch.cuda.synchronize()
 
     for _ in range(args.warmup):
         step()
@@ -262,8 +276,8 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
 
-    # per-kernel times from the events (the dQ zeroing is in the step, outside the kernel intervals)
-    span = lambda a, b: sorted(e[a].elapsed_time(e[b]) for e in events)
+    # per-kernel times from the events
+    span = lambda a, b, evs=events: sorted(e[a].elapsed_time(e[b]) for e in evs)
     fwd_ms, cd_ms, kv_ms, dq_ms, bwd_ms = span(0, 1), span(1, 2), span(2, 3), span(3, 4), span(2, 4)
     avg = lambda xs: sum(xs) / len(xs)
     med = lambda xs: xs[len(xs) // 2]
@@ -274,8 +288,13 @@ def main():
     # dominant kernel: the dK/dV kernel (4 products: S, dP, dV = P^T dO, dK = dS^T Q)
     kv_avg = avg(kv_ms)
     achieved = 4.0 * unit / (kv_avg * 1e-3) / 1e12
-
+    # dQ kernel from the stored dS: reads every dS tile once, K (once per 128-query block, from L2
+    # after the first), writes dQ fp32 once; algorithmic bytes = dS + K + dQ
     bthd = B * T * H * D
+    dq_bytes = ws_bytes + 2 * bthd + 4 * bthd
+    dq_avg = avg(dq_ms)
+    rc_kv, rc_dq, rc_bwd = span(2, 3, rc_events), span(3, 4, rc_events), span(2, 4, rc_events)
+
     result = {
         "metric": "causal attn fwd+bwd TFLOP/s at B,H,T,D bf16; % of MI355X bf16 MFMA peak",
         "value": round(value, 2),
@@ -296,20 +315,34 @@ def main():
             "fwd_ms_median": round(med(fwd_ms), 4), "computeD_ms_median": round(med(cd_ms), 4),
             "bwd_ms_median": round(med(bwd_ms), 4), "bwd_dkdv_ms_median": round(med(kv_ms), 4),
             "bwd_dq_ms_median": round(med(dq_ms), 4),
+            "bwd_recompute_ms_median": round(med(rc_bwd), 4), "bwd_recompute_dkdv_ms_median": round(med(rc_kv), 4),
+            "bwd_recompute_dq_ms_median": round(med(rc_dq), 4),
+            "workspace_bytes": ws_bytes,
             "fwd_tflops": round(ff / (med(fwd_ms) * 1e-3) / 1e12, 2),
             "bwd_tflops": round(fb / (med(bwd_ms) * 1e-3) / 1e12, 2),
             "computeD_gbs": round((4 * bthd + 4 * B * H * T) / (med(cd_ms) * 1e-3) / 1e9, 1),
         },
         "roofline": {
-            "kernel": "flashAttentionBackward dK/dV kernel (mla::bwd_kernel)",
+            "kernel": "backward dK/dV kernel with the dS store (mla::bwd_kernel<D, true>)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic_from_profiles(args.config),
-            "algorithmic_bytes": 12 * bthd + 8 * B * H * T,
+            "algorithmic_bytes": 12 * bthd + 8 * B * H * T + ws_bytes,
             "avg_ms": round(kv_avg, 4),
+        },
+        "roofline_dq": {
+            "kernel": "backward dQ kernel from the stored dS (mla::dqs_kernel)",
+            "bound": "hbm",
+            "achieved": round(dq_bytes / (dq_avg * 1e-3) / 1e9, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(dq_bytes / (dq_avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profiles(args.config, "dqs"),
+            "algorithmic_bytes": dq_bytes,
+            "avg_ms": round(dq_avg, 4),
         },
     }
     if not args.no_cpu_baseline:

@@ -12,14 +12,16 @@
  *   q, k, v, out, dO, dK, dV : bf16 bit patterns, [B, T, NH, D] (one token row = N = NH*D elements;
  *                              for B = 1 this is the reference's [T, N] buffer)
  *   l (logsumexp), D         : fp32 [B, NH, T] (the reference indexes them [t*NH + h], one sequence)
- *   dQ                       : fp32 [B, T, NH, D], ACCUMULATED into with atomics: the caller zeroes
- *                              it first, as model.h:549 does
- * dK and dV are written in full (the reference accumulates into caller-zeroed buffers,
- * model.h:550-551; the result is the same). D holds the bf16-rounded value of rowsum(dO*O),
- * stored as fp32.
+ *   dQ                       : fp32 [B, T, NH, D]
+ * dQ, dK and dV are written in full: the reference accumulates them into buffers the caller
+ * zeroed (dQ with fp32 atomics; model.h:549-551 zeroes all three before every backward), which
+ * gives the same result; here each element has one owner that writes it once, so the backward
+ * is deterministic and the zeroing is not needed. D holds the bf16-rounded value of
+ * rowsum(dO*O), stored as fp32.
  *
  * Semantics: asynchronous on `stream` (NULL = the default stream); no allocation, no host
- * synchronisation, no global state, so calls on distinct streams may run concurrently. Each
+ * synchronisation, no global state, so calls on distinct streams may run concurrently (the
+ * workspace variant's workspace belongs to one call at a time). Each
  * entry point validates its arguments before touching the device and returns METALLLM_ATTN_OK or
  * a negative error code; a failed kernel launch returns METALLLM_ATTN_E_LAUNCH.
  * Supported shapes: M (= T) a positive multiple of 64, D in {64, 128}, N == NH*D, B >= 1,
@@ -69,11 +71,30 @@ int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionPar
              metalllm_stream_t stream);
 
 /* Replaces the flashAttentionBackward dispatch at model.h:648-665 (attention.metal:198-299).
- * dZ is dO; d and l are computeD's and the forward's outputs. dQ += gradient (fp32 atomics);
- * dK, dV = gradients (bf16). */
+ * dZ is dO; d and l are computeD's and the forward's outputs. dQ = gradient (fp32); dK, dV =
+ * gradients (bf16). Two kernels: dK/dV by key-block owners, then dQ by query-block owners, each
+ * recomputing the softmax tile it needs. */
 int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                            const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                            const AttentionParams* p, metalllm_stream_t stream);
+
+/* Bytes of device workspace flashAttentionBackwardWorkspace needs for shape p: one 64x64 bf16
+ * dS tile per (query tile, key tile <= query tile) of every (b, head), i.e.
+ * B*NH*(M/64)*(M/64+1)/2 * 8192 (4.4e9 at B = NH = 16, M = 4096). No counterpart in the
+ * reference (its backward keeps dS in threadgroup memory). */
+int metalllmAttnBackwardWorkspaceSize(const AttentionParams* p, uint64_t* bytes);
+
+/* The same backward as flashAttentionBackward (model.h:648-665), faster at long sequences: the
+ * dK/dV kernel also stores every bf16 dS tile it computes into `workspace` (device memory, 16-byte
+ * aligned, at least metalllmAttnBackwardWorkspaceSize bytes), and dQ = dS.K then streams those
+ * tiles instead of recomputing the softmax. dK and dV are bit-identical to flashAttentionBackward's;
+ * dQ differs only by fp32 summation order. The workspace holds no state between calls, but one
+ * workspace must not serve two calls at once. Returns METALLLM_ATTN_E_NULL / _E_ALIGN / _E_SIZE
+ * for a NULL, misaligned or too small workspace. No counterpart in the reference. */
+int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                                    const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                                    void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
+                                    metalllm_stream_t stream);
 
 /* ---- The sublayer around the attention core (attention.metal:19-53, 301-455) ----
  * Plain GEMMs with the reference kernels' names and buffer order. Row-major: X, attn_out (O), dZ,
@@ -106,7 +127,7 @@ int projBackwarddX(const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, 
                    metalllm_stream_t stream);
 
 /* attention.metal:301-341, model.h:666-677: dX += dQ.q_w^T + dK.k_w^T + dV.v_w^T (fp32, accumulated;
- * dQ is the fp32 accumulator flashAttentionBackward produced). */
+ * dQ is the fp32 gradient flashAttentionBackward produced). */
 int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
                   const uint16_t* dK, const uint16_t* dV, const AttentionParams* p, metalllm_stream_t stream);
 
@@ -139,7 +160,7 @@ typedef struct metalllmSublayerBuffers {
   const uint16_t* dOut;   /* bf16 gradient at the sublayer output (model.h's dBranch, :622)    */
   uint16_t* dAttn;        /* bf16 gradient at O (model.h's dZAttn, :633)                       */
   float* Dsum;            /* fp32 computeD output                                               */
-  float* dQ;              /* fp32 accumulator                                                   */
+  float* dQ;              /* fp32                                                               */
   uint16_t* dK;           /* bf16                                                               */
   uint16_t* dV;
   float* dX;              /* fp32 gradient at X (model.h's dXAttn)                              */
@@ -154,17 +175,19 @@ typedef struct metalllmSublayerGraph metalllmSublayerGraph;
 
 /* Enqueues one phase of the sublayer on `stream`, in model.h's order.
  *   phase 0 (model.h:444-483): computeQKV, flashAttentionForward, projForward.
- *   phase 1 (model.h:549-555, 620-693): zero dQ, dX, dQw, dKw, dVw, dProjw; projBackwarddW,
- *            projBackwarddX, computeD, flashAttentionBackward, computeGradDx, computeGradDw (one
- *            two-term split of dQ serves both), and castFloatToBfloat(dX) when dX_bf16 is set.
+ *   phase 1 (model.h:549-555, 620-693): zero dX, dQw, dKw, dVw, dProjw; projBackwarddW,
+ *            projBackwarddX, computeD, flashAttentionBackwardWorkspace, computeGradDx,
+ *            computeGradDw (one two-term split of dQ serves both), and castFloatToBfloat(dX) when
+ *            dX_bf16 is set.
  * Validation: the GEMM rules and the attention rules above, every pointer the phase uses.
- * Uses the device's shared rocBLAS handle and scratch like the GEMM entry points above. */
+ * Uses the device's shared rocBLAS handle and scratch like the GEMM entry points above (plus a
+ * per-device attention workspace, metalllmAttnBackwardWorkspaceSize bytes, grown on demand). */
 int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
                            metalllm_stream_t stream);
 
 /* Records the same phase once as a HIP graph (pointers and shapes fixed at creation) and returns
  * it in *out; metalllmSublayerGraphLaunch replays it on `stream` with one launch, reading the
- * buffers' current contents. A graph owns its rocBLAS handle, workspace and scratch (allocated
+ * buffers' current contents. A graph owns its rocBLAS handle, workspaces and scratch (allocated
  * here, freed by Destroy), so it never depends on memory other calls may reallocate. Replays of
  * one graph must not overlap each other; Destroy only after the last replay completed. These
  * three have no single counterpart in the reference (it re-encodes the command buffer each step,
@@ -174,14 +197,17 @@ int metalllmSublayerGraphCreate(int phase, const metalllmSublayerBuffers* b, con
 int metalllmSublayerGraphLaunch(metalllmSublayerGraph* g, metalllm_stream_t stream);
 int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g);
 
-/* Bench hook (no counterpart in the reference): launches one of the two kernels that
- * flashAttentionBackward runs, in this order, on `stream`: part 0 = dK/dV (key-block owners),
- * part 1 = dQ (query-block owners). flashAttentionBackward(args) is exactly part 0 followed by
- * part 1, so timing the parts separately measures the same work. Same arguments, validation and
- * return codes as flashAttentionBackward; part outside {0, 1} returns METALLLM_ATTN_E_LAYOUT. */
+/* Bench hook (no counterpart in the reference): launches one of the kernels of the two backward
+ * entry points on `stream`: part 0 = dK/dV and part 1 = dQ recomputing the softmax
+ * (flashAttentionBackward is exactly part 0 then part 1); part 2 = dK/dV storing dS into the
+ * workspace and part 3 = dQ from the stored dS (flashAttentionBackwardWorkspace is exactly part 2
+ * then part 3). Timing the parts separately measures the same work. Same validation and return
+ * codes as those entry points (parts 0 and 1 ignore the workspace arguments); a part outside
+ * 0..3 returns METALLLM_ATTN_E_LAYOUT. */
 int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                              const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
-                             const AttentionParams* p, metalllm_stream_t stream);
+                             void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
+                             metalllm_stream_t stream);
 
 /* Static description of an error code (no counterpart in the reference, which has no error
  * path per kernel; model.h:333-336,361-365 only print). */

@@ -4,9 +4,11 @@ The product is libmetalllm_attn.so (C ABI in include/metalllm_attn.h); this pack
 (`metalllm_amd.build`) and binds it (`metalllm_amd.attention`).
 """
 from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, backward_part,
-                        computeD, flashAttentionBackward, flashAttentionForward, library, work_map)
+                        computeD, flashAttentionBackward, flashAttentionBackwardWorkspace, flashAttentionForward,
+                        library, work_map, workspace_bytes)
 
 from . import sublayer  # noqa: E402  (the GEMMs around the attention core)
 
 __all__ = ["sublayer", "AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
-           "computeD", "flashAttentionBackward", "flashAttentionForward", "library", "work_map"]
+           "computeD", "flashAttentionBackward", "flashAttentionBackwardWorkspace", "flashAttentionForward", "library",
+           "work_map", "workspace_bytes"]

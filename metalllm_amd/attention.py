@@ -2,7 +2,9 @@
 
 The three entry points mirror the reference's kernels and their dispatch sites
 (/root/reference/attention.metal:56-299, /root/reference/model.h:459-473,639-665): same names,
-same buffer order, caller-owned buffers, dQ accumulated into (caller zeroes it). PyTorch only
+same buffer order, caller-owned buffers; dQ, dK and dV written in full (the reference's
+accumulation into zeroed buffers gives the same result), and a faster backward variant with a
+caller-provided device workspace (flashAttentionBackwardWorkspace). PyTorch only
 provides device memory and the stream; every computation happens in the HIP kernels. There is
 no CPU fallback: if the library is missing, or a tensor is not on a GPU, these functions raise.
 
@@ -25,6 +27,7 @@ ERRORS = {
 EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
             "metalllmAttnErrorString", "metalllmAttnWorkMap", "computeQKV", "projForward", "projBackwarddW",
             "projBackwarddX", "computeGradDx", "computeGradDw", "castFloatToBfloat", "metalllmSublayerEncode",
+            "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize",
             "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy")
 
 
@@ -58,8 +61,12 @@ def _lib():
         L.flashAttentionForward.argtypes = [vp, vp, vp, vp, vp, pp, vp]
         L.computeD.argtypes = [vp, vp, vp, pp, vp]
         L.flashAttentionBackward.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, pp, vp]
-        L.metalllmAttnBackwardPart.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, pp, vp]
-        for f in (L.flashAttentionForward, L.computeD, L.flashAttentionBackward, L.metalllmAttnBackwardPart):
+        u64 = ctypes.c_uint64
+        L.metalllmAttnBackwardPart.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u64, pp, vp]
+        L.flashAttentionBackwardWorkspace.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u64, pp, vp]
+        L.metalllmAttnBackwardWorkspaceSize.argtypes = [pp, ctypes.POINTER(u64)]
+        for f in (L.flashAttentionForward, L.computeD, L.flashAttentionBackward, L.metalllmAttnBackwardPart,
+                  L.flashAttentionBackwardWorkspace, L.metalllmAttnBackwardWorkspaceSize):
             f.restype = ctypes.c_int
         L.metalllmAttnErrorString.argtypes = [ctypes.c_int]
         L.metalllmAttnErrorString.restype = ctypes.c_char_p
@@ -115,18 +122,46 @@ def computeD(dO, O, D, stream=None, params: AttentionParams | None = None):
 
 
 def flashAttentionBackward(dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None):
-    """attention.metal:198-299. dQ += grad (fp32, caller zeroes); dK, dV = grads (bf16)."""
+    """attention.metal:198-299. dQ = grad (fp32); dK, dV = grads (bf16); all three written in full."""
     p = params or _shape(q)
     _check(_lib().flashAttentionBackward(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ), _ptr(dK),
                                          _ptr(dV), ctypes.byref(p), _stream(stream)), "flashAttentionBackward")
 
 
-def backward_part(part: int, dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None):
-    """One of the two kernels of flashAttentionBackward (0: dK/dV, 1: dQ); the bench times them
-    separately. Running part 0 then part 1 is flashAttentionBackward."""
+def workspace_bytes(B: int, T: int, H: int, D: int) -> int:
+    """Device workspace flashAttentionBackwardWorkspace needs (bytes)."""
+    n = ctypes.c_uint64()
+    _check(_lib().metalllmAttnBackwardWorkspaceSize(ctypes.byref(AttentionParams.of(B, T, H, D)), ctypes.byref(n)),
+           "metalllmAttnBackwardWorkspaceSize")
+    return n.value
+
+
+def _ws(workspace):
+    if workspace is None:
+        return None, 0
+    return _ptr(workspace), workspace.numel() * workspace.element_size()
+
+
+def flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, workspace, stream=None,
+                                    params: AttentionParams | None = None):
+    """flashAttentionBackward with a device workspace (a tensor of at least workspace_bytes bytes)
+    holding the stored dS tiles; dK, dV identical, dQ equal up to fp32 summation order."""
     p = params or _shape(q)
+    wp, wn = _ws(workspace)
+    _check(_lib().flashAttentionBackwardWorkspace(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
+                                                  _ptr(dK), _ptr(dV), wp, wn, ctypes.byref(p), _stream(stream)),
+           "flashAttentionBackwardWorkspace")
+
+
+def backward_part(part: int, dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None,
+                  workspace=None):
+    """One kernel of the backward entry points (0: dK/dV, 1: dQ recomputing the softmax = the two
+    kernels of flashAttentionBackward; 2: dK/dV storing dS into `workspace`, 3: dQ from the stored
+    dS = flashAttentionBackwardWorkspace); the bench times them separately."""
+    p = params or _shape(q)
+    wp, wn = _ws(workspace)
     _check(_lib().metalllmAttnBackwardPart(part, _ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
-                                           _ptr(dK), _ptr(dV), ctypes.byref(p), _stream(stream)),
+                                           _ptr(dK), _ptr(dV), wp, wn, ctypes.byref(p), _stream(stream)),
            "metalllmAttnBackwardPart")
 
 
@@ -141,11 +176,11 @@ def attention_forward(q, k, v, stream=None):
 
 
 def attention_backward(dO, q, k, v, out, lse, stream=None):
-    """The reference's backward sequence (model.h:549-551 zeroing, :639-665 dispatches):
-    dQ zeroed, computeD, flashAttentionBackward. Returns (dQ fp32, dK, dV, D)."""
+    """The reference's backward sequence (model.h:639-665 dispatches): computeD,
+    flashAttentionBackward. Returns (dQ fp32, dK, dV, D)."""
     import torch
     B, T, H, D = q.shape
-    dQ = torch.zeros((B, T, H, D), dtype=torch.float32, device=q.device)
+    dQ = torch.empty((B, T, H, D), dtype=torch.float32, device=q.device)
     dK = torch.empty_like(q)
     dV = torch.empty_like(q)
     Dv = torch.empty((B, H, T), dtype=torch.float32, device=q.device)

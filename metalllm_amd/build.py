@@ -16,14 +16,13 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmetalllm_attn.so")
-SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_computed.hip", "sublayer.hip", "glue.hip"]
+SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_bwd_dqs.hip", "attn_computed.hip", "sublayer.hip", "glue.hip"]
 LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]  # sublayer GEMMs
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",            # keep the reference's separate multiply/add roundings
-    "-munsafe-fp-atomics",          # hardware global_atomic_add_f32 for the dQ accumulator
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"),
 ]

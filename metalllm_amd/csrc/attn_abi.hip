@@ -2,6 +2,7 @@
 // include/metalllm_attn.h). Validation happens on the host before any HIP call, so argument
 // errors are reported without touching the device.
 #include <cmath>
+
 #include "../../include/metalllm_attn.h"
 #include "attn_launch.hpp"
 
@@ -46,19 +47,35 @@ int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionPar
                                                                                 : METALLLM_ATTN_E_LAUNCH;
 }
 
-int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
-                             const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
-                             const AttentionParams* p, metalllm_stream_t stream) {
+int metalllmAttnBackwardWorkspaceSize(const AttentionParams* p, uint64_t* bytes) {
   const int rc = validate(p);
   if (rc) return rc;
-  if (part != 0 && part != 1) return METALLLM_ATTN_E_LAYOUT;
+  if (!bytes) return METALLLM_ATTN_E_NULL;
+  *bytes = (uint64_t)mla::ds_scratch_bytes((int)p->B, (int)p->NH, (int)p->M);
+  return METALLLM_ATTN_OK;
+}
+
+int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                             const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                             void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
+                             metalllm_stream_t stream) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (part < 0 || part > 3) return METALLLM_ATTN_E_LAYOUT;
   if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
   if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
     return METALLLM_ATTN_E_ALIGN;
   mla::BwdArgs a{dZ, d, l, q, k, v, dQ, dK, dV, (int)p->M, (int)p->NH, (int)p->B, head_scale(p->D)};
-  const hipError_t e = part == 0 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
-                                 : mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream);
+  if (part >= 2) {
+    if (!workspace) return METALLLM_ATTN_E_NULL;
+    if (!aligned16(workspace)) return METALLLM_ATTN_E_ALIGN;
+    if (workspace_bytes < (uint64_t)mla::ds_scratch_bytes(a.B, a.H, a.T)) return METALLLM_ATTN_E_SIZE;
+    a.dS = (uint16_t*)workspace;
+  }
+  const hipError_t e = part == 0 || part == 2 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
+                       : part == 1           ? mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream)
+                                             : mla::launch_backward_dqs(a, (int)p->D, (hipStream_t)stream);
   return e == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
@@ -66,9 +83,19 @@ int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, c
                            const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                            const AttentionParams* p, metalllm_stream_t stream) {
   // dK/dV by the key-block owners, then dQ by the query-block owners (both on `stream`, in order)
-  const int rc = metalllmAttnBackwardPart(0, dZ, d, l, q, k, v, dQ, dK, dV, p, stream);
+  const int rc = metalllmAttnBackwardPart(0, dZ, d, l, q, k, v, dQ, dK, dV, nullptr, 0, p, stream);
   if (rc) return rc;
-  return metalllmAttnBackwardPart(1, dZ, d, l, q, k, v, dQ, dK, dV, p, stream);
+  return metalllmAttnBackwardPart(1, dZ, d, l, q, k, v, dQ, dK, dV, nullptr, 0, p, stream);
+}
+
+int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                                    const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                                    void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
+                                    metalllm_stream_t stream) {
+  // dK/dV by the key-block owners, storing dS into the workspace; then dQ = dS.K
+  const int rc = metalllmAttnBackwardPart(2, dZ, d, l, q, k, v, dQ, dK, dV, workspace, workspace_bytes, p, stream);
+  if (rc) return rc;
+  return metalllmAttnBackwardPart(3, dZ, d, l, q, k, v, dQ, dK, dV, workspace, workspace_bytes, p, stream);
 }
 
 const char* metalllmAttnErrorString(int code) {

@@ -6,8 +6,10 @@
 //   p = exp(S*scale - lse[q]), p = 0 where key > q (diagonal), P = bf16(p)
 //   dS = bf16(p * (dP - D[q]) * scale)                            (:277-286)
 //   dK = bf16(dK + dS^T.Q), dV = bf16(dV + P^T.dO)   once per query tile (:289-290)
-// The key-tile owner accumulates dK/dV race-free. dQ (:288,292-296) is computed by the
-// query-owner kernel in attn_bwd_dq.hip, which flashAttentionBackward launches after this one.
+// The key-tile owner accumulates dK/dV race-free. dQ (:288,292-296) is computed by a query-owner
+// kernel launched after this one: attn_bwd_dq.hip recomputes dS (flashAttentionBackward), or,
+// when the caller provides a workspace (flashAttentionBackwardWorkspace), this kernel also
+// stores every dS tile it computes, bf16, and attn_bwd_dqs.hip computes dQ = dS.K from them.
 //
 // Work split: 4 waves x 32 keys per workgroup, two workgroups per CU. Wave w owns keys
 // 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core B operands
@@ -65,7 +67,7 @@ struct DiagTag {
   static constexpr bool value = V;
 };
 
-template <int D>
+template <int D, bool DS>
 __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
@@ -185,7 +187,22 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
   //   [2KC, 3KC) S of rows 32-63           [3KC, 4KC) dP of rows 32-63
   //   [4KC, NS) update chain n = (i - 4KC) / 4, query step j = (i - 4KC) % 4
   // S[t], dP[t] hold rows q = 32t + 8(r/4) + 4h + r%4 of the tile, lane = key.
-  auto qtile = [&](int qb, int stage, auto diag_tag) {
+  // dS of the latest query tile, packed bf16 (index 8t + r/2); with DS it is stored in the first
+  // slots of the next tile (or after the last one), so the end-of-tile wait never waits for it
+  uint32_t dS[16];
+  // this wave's 32 keys are half hw of key tile ktw; dS tile (qt, ktw) of the pair's triangle
+  const int ktw = kb * (C::BN / 64) + (wave >> 1), hw = wave & 1;
+  const int nqt = a.T / 64;
+  const size_t tri = (size_t)pair * ((size_t)nqt * (nqt + 1) / 2);
+  auto ds_addr = [&](int qt) -> char* {
+    if (!DS || !wave_keys || ktw > qt) return nullptr;
+    return (char*)a.dS + (tri + (size_t)qt * (qt + 1) / 2 + ktw) * 8192 + hw * 4096 + lane * 16;
+  };
+  auto store_ds = [&](char* dst, int s) {  // streaming store: the tile is read once, by another kernel
+    __builtin_nontemporal_store(u32x4{dS[4 * s], dS[4 * s + 1], dS[4 * s + 2], dS[4 * s + 3]}, (u32x4*)(dst + 1024 * s));
+  };
+
+  auto qtile = [&](int qb, int stage, auto diag_tag, char* ds_prev) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     constexpr int NS = 4 * C::KC + 8 * C::DT;
     constexpr int PPS = 8 / C::KC;  // score pairs of vector work per S/dP slot
@@ -198,7 +215,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
     pin(stat_a);
     const int qrow = qb * C::BM + 4 * h - key;  // q - key = qrow + 32t + 8g + i
     f32x16 x0 = zero16(), x1 = zero16(), y0 = zero16(), y1 = zero16();
-    uint32_t Pp[16], dS[16];  // packed bf16: index 8t + r/2
+    uint32_t Pp[16];  // packed bf16: index 8t + r/2
 
     auto operand = [&](int i) -> u32x4 {
       if (i < 4 * C::KC) {
@@ -302,6 +319,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
         else if (w.kind == 2)
           ds_pair(w.t ? x1 : x0, w.t ? y1 : y0, w.t, w.u0 + v, st[2 * v], st[2 * v + 1]);
       }
+      if (DS && i < 4 && ds_prev) store_ds(ds_prev, i);  // previous tile's dS (rewritten from slot 2KC on)
       if (i < C::KC) {
         // the previous tile's last chain (dK of d tile DT-1, block 1) back into the state
         pack_pairs(2 * C::DT - 1, (i * 8) / C::KC, ((i + 1) * 8) / C::KC);
@@ -329,21 +347,26 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
   scale_lse(0);
   __syncthreads();
   int qb = qb0, it = 0;
+  char* ds_prev = nullptr;
   for (; qb < nqb && qb < qb0 + 2; ++qb, ++it) {
     if (qb + 1 < nqb) issue_tile(qb + 1, (it + 1) & 1);
-    qtile(qb, it & 1, DiagTag<true>());
+    qtile(qb, it & 1, DiagTag<true>(), ds_prev);
+    ds_prev = ds_addr(qb);
     __builtin_amdgcn_s_waitcnt(0);
     if (qb + 1 < nqb) scale_lse((it + 1) & 1);
     __syncthreads();
   }
   for (; qb < nqb; ++qb, ++it) {
     if (qb + 1 < nqb) issue_tile(qb + 1, (it + 1) & 1);
-    qtile(qb, it & 1, DiagTag<false>());
+    qtile(qb, it & 1, DiagTag<false>(), ds_prev);
+    ds_prev = ds_addr(qb);
     __builtin_amdgcn_s_waitcnt(0);
     if (qb + 1 < nqb) scale_lse((it + 1) & 1);
     __syncthreads();
   }
   pack_pairs(2 * C::DT - 1, 0, 8);
+  if (DS && ds_prev)
+    for (int s = 0; s < 4; ++s) store_ds(ds_prev, s);
 
   // ---- dK, dV: lane = key, rows d = 32dt + 8g + 4h + i ----
   if (!wave_keys) return;
@@ -362,10 +385,17 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
 hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s) {
   const int nkb = (a.T + kBwdBlockN - 1) / kBwdBlockN;
   const dim3 grid((unsigned)(a.B * a.H * nkb));
-  if (D == 64)
-    hipLaunchKernelGGL(bwd_kernel<64>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(bwd_kernel<128>, grid, dim3(256), 0, s, a);
+  if (a.dS) {
+    if (D == 64)
+      hipLaunchKernelGGL((bwd_kernel<64, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_kernel<128, true>), grid, dim3(256), 0, s, a);
+  } else {
+    if (D == 64)
+      hipLaunchKernelGGL((bwd_kernel<64, false>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_kernel<128, false>), grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

@@ -36,12 +36,23 @@ struct BwdArgs {
   uint16_t* dV;
   int T, H, B;
   float scale;
+  // Optional: the dS tiles of the causal lower triangle, bf16, written by launch_backward and
+  // read by launch_backward_dqs (ds_scratch_bytes(); layout in attn_bwd_dqs.hip). NULL: not stored.
+  uint16_t* dS = nullptr;
 };
+
+// Bytes of the dS tile store for B*H pairs of T rows: one 64x64 bf16 tile per (query tile,
+// key tile <= query tile) of every pair.
+inline size_t ds_scratch_bytes(int B, int H, int T) {
+  const size_t nqt = (size_t)T / 64;
+  return (size_t)B * H * (nqt * (nqt + 1) / 2) * 8192;
+}
 
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s);
 hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
 hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);     // dK, dV (key-owner)
 hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s);  // dQ (query-owner)
+hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s); // dQ from the stored dS
 
 // Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
 // spread so that every block of one pair lands on the same XCD (workgroups are handed to the

@@ -49,6 +49,8 @@ struct DeviceState {
   size_t split_elems = 0;
   float* partial = nullptr;   // fp32 partial products of the weight gradients [parts][C][C]
   size_t partial_elems = 0;
+  uint8_t* attn_ws = nullptr;  // the attention backward's dS tiles (metalllmSublayerEncode)
+  size_t attn_ws_bytes = 0;
 };
 
 // Grows a per-device buffer (never shrinks; the old one is freed after the device drained).
@@ -376,14 +378,16 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
 // MI355X form is a HIP graph per phase of the attention sublayer: the launches are recorded once
 // on a private stream with the pointers and shapes baked in, and replayed with one launch. Each
 // graph owns its rocBLAS handle, that handle's workspace (sized by a rocBLAS size query before
-// capture) and its scratch (dQ split, weight-gradient partials), so nothing a replay touches is
-// ever reallocated by other calls.
+// capture) and its scratch (dQ split, weight-gradient partials, the attention backward's dS
+// tiles), so nothing a replay touches is ever reallocated by other calls.
 struct metalllmSublayerGraph {
   int phase = 0;
   rocblas_handle h = nullptr;
   void* workspace = nullptr;
   uint16_t* split = nullptr;
   float* partial = nullptr;
+  void* attn_ws = nullptr;
+  uint64_t attn_ws_bytes = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 };
@@ -408,7 +412,7 @@ int check_phase(int phase, const metalllmSublayerBuffers* b, const AttentionPara
 
 // The launch sequence of one phase (model.h:444-483 forward, :549-555 and :620-693 backward).
 int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const AttentionParams* p, uint16_t* split,
-           float* partial) {
+           float* partial, void* attn_ws, uint64_t attn_ws_bytes) {
   const int R = (int)(p->B * p->M), C = (int)p->N;
   const size_t e = (size_t)R * C;
   const metalllm_stream_t s = (metalllm_stream_t)c.stream;
@@ -417,8 +421,8 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
     if (!c.query) TRY(flashAttentionForward(b->q, b->k, b->v, b->attn_out, b->l, p, s));
     return op_proj_fwd(c, b->attn_out, b->proj_w, b->out, R, C);
   }
-  // model.h:549-555 zeroes the accumulated gradients before the pass (dK and dV are written in full)
-  TRY(zero_bytes(c, b->dQ, e * 4));
+  // model.h:549-555 zeroes the accumulated gradients before the pass (the attention backward
+  // writes dQ, dK and dV in full)
   TRY(zero_bytes(c, b->dX, e * 4));
   TRY(zero_bytes(c, b->dQw, (size_t)C * C * 4));
   TRY(zero_bytes(c, b->dKw, (size_t)C * C * 2));
@@ -428,7 +432,8 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
   if (!c.query) {
     TRY(computeD(b->dAttn, b->attn_out, b->Dsum, p, s));
-    TRY(flashAttentionBackward(b->dAttn, b->Dsum, b->l, b->q, b->k, b->v, b->dQ, b->dK, b->dV, p, s));
+    TRY(flashAttentionBackwardWorkspace(b->dAttn, b->Dsum, b->l, b->q, b->k, b->v, b->dQ, b->dK, b->dV, attn_ws,
+                                        attn_ws_bytes, p, s));
   }
   TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
   TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, split, split + e, b->dK, b->dV, R, C));
@@ -447,7 +452,9 @@ int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, cons
     if (hipMalloc((void**)&g->split, 2 * (size_t)R * C * sizeof(uint16_t)) != hipSuccess) g->split = nullptr;
     if (hipMalloc((void**)&g->partial, 2 * (size_t)row_chunks(R) * C * C * sizeof(float)) != hipSuccess)
       g->partial = nullptr;
-    if (!g->split || !g->partial) return METALLLM_ATTN_E_LIBRARY;
+    TRY(metalllmAttnBackwardWorkspaceSize(p, &g->attn_ws_bytes));
+    if (hipMalloc(&g->attn_ws, g->attn_ws_bytes) != hipSuccess) g->attn_ws = nullptr;
+    if (!g->split || !g->partial || !g->attn_ws) return METALLLM_ATTN_E_LIBRARY;
   }
   // the workspace the phase's rocBLAS calls need, owned by the graph
   size_t ws = 0;
@@ -455,7 +462,7 @@ int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, cons
   Ctx q;
   q.h = g->h;
   q.query = true;
-  const int qrc = encode(q, g->phase, b, p, g->split, g->partial);
+  const int qrc = encode(q, g->phase, b, p, g->split, g->partial, g->attn_ws, g->attn_ws_bytes);
   if (rocblas_stop_device_memory_size_query(g->h, &ws) != rocblas_status_success || qrc) return METALLLM_ATTN_E_LIBRARY;
   if (ws && hipMalloc(&g->workspace, ws) != hipSuccess) {
     g->workspace = nullptr;
@@ -470,7 +477,7 @@ int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, cons
     Ctx c;
     c.h = g->h;
     c.stream = cap;
-    rc = encode(c, g->phase, b, p, g->split, g->partial);
+    rc = encode(c, g->phase, b, p, g->split, g->partial, g->attn_ws, g->attn_ws_bytes);
     const hipError_t e = hipStreamEndCapture(cap, &g->graph);  // always ends the capture
     if (!rc && e != hipSuccess) rc = METALLLM_ATTN_E_LIBRARY;
   }
@@ -489,11 +496,14 @@ int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const At
   const int R = (int)(p->B * p->M), C = (int)p->N;
   Public u(stream);
   TRY(u.s.rc);
+  uint64_t ws = 0;
   if (phase == 1) {
     TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C));
     TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C));
+    TRY(metalllmAttnBackwardWorkspaceSize(p, &ws));
+    TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws));
   }
-  return encode(u.c, phase, b, p, u.s.st->split, u.s.st->partial);
+  return encode(u.c, phase, b, p, u.s.st->split, u.s.st->partial, u.s.st->attn_ws, ws);
 }
 
 int metalllmSublayerGraphCreate(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
@@ -525,6 +535,7 @@ int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g) {
   if (g->workspace) (void)hipFree(g->workspace);
   if (g->split) (void)hipFree(g->split);
   if (g->partial) (void)hipFree(g->partial);
+  if (g->attn_ws) (void)hipFree(g->attn_ws);
   delete g;
   return METALLLM_ATTN_OK;
 }

@@ -14,8 +14,8 @@ from __future__ import annotations
 
 import ctypes
 
-from .attention import (AttentionParams, _check, _lib, _ptr, _stream, attention_forward, backward_part, computeD,
-                        flashAttentionForward)
+from .attention import (AttentionParams, _check, _lib, _ptr, _stream, backward_part, computeD, flashAttentionForward,
+                        workspace_bytes)
 
 _BOUND = False
 
@@ -155,7 +155,8 @@ class Sublayer:
         self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.dO, self.dK, self.dV = bf(), bf(), bf()
         self.Dv = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-        self.dQ = torch.zeros((B, T, C), dtype=torch.float32, device=dev)
+        self.dQ = torch.empty((B, T, C), dtype=torch.float32, device=dev)
+        self.ws = torch.empty((workspace_bytes(B, T, H, D),), dtype=torch.uint8, device=dev)
         self.dX = torch.zeros((B, T, C), dtype=torch.float32, device=dev)
         self.dWq = torch.zeros((C, C), dtype=torch.float32, device=dev)
         self.dWk = torch.zeros((C, C), dtype=torch.bfloat16, device=dev)
@@ -207,7 +208,7 @@ class Sublayer:
         return self.out
 
     def zero_grads(self):
-        for t in (self.dQ, self.dX, self.dWq, self.dWk, self.dWv, self.dWp):
+        for t in (self.dX, self.dWq, self.dWk, self.dWv, self.dWp):
             t.zero_()
 
     def backward(self, dOut, stream=None, parts=None):
@@ -219,8 +220,11 @@ class Sublayer:
         projBackwarddX(dOut, self.Wp, self.dO, p, stream)
         mark("proj")
         computeD(self.dO, self.o, self.Dv, stream, p)
-        backward_part(0, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p)
-        backward_part(1, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p)
+        # flashAttentionBackwardWorkspace, as its two kernels (the bench times them separately)
+        backward_part(2, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p,
+                      workspace=self.ws)
+        backward_part(3, self.dO, self.Dv, self.lse, self.q, self.k, self.v, self.dQ, self.dK, self.dV, stream, p,
+                      workspace=self.ws)
         mark("attention")
         computeGradDx(self.dX, self.Wq, self.Wk, self.Wv, self.dQ, self.dK, self.dV, p, stream)
         computeGradDw(self.X, self.dQ, self.dK, self.dV, self.dWq, self.dWk, self.dWv, p, stream)

@@ -44,15 +44,21 @@ def gpu_forward(q, k, v, dev):
     return to_np(out), to_np(lse)
 
 
-def gpu_backward(g, Dv, lse, q, k, v, dev):
-    """flashAttentionBackward alone on given D / lse (dQ zeroed first)."""
+def gpu_backward(g, Dv, lse, q, k, v, dev, workspace=False):
+    """flashAttentionBackward (or, with workspace, flashAttentionBackwardWorkspace) alone on given
+    D / lse. The outputs start filled with NaN: the backward writes them in full."""
     import torch
     import metalllm_amd as M
     tq, tk, tv, tg = (to_gpu(x, dev) for x in (q, k, v, g))
-    dQ = torch.zeros(q.shape, dtype=torch.float32, device=dev)
-    dK = torch.empty_like(tq)
-    dV = torch.empty_like(tq)
-    M.flashAttentionBackward(tg, to_gpu(Dv, dev), to_gpu(lse, dev), tq, tk, tv, dQ, dK, dV)
+    dQ = torch.full(q.shape, float("nan"), dtype=torch.float32, device=dev)
+    dK = torch.full_like(tq, float("nan"))
+    dV = torch.full_like(tq, float("nan"))
+    if workspace:
+        B, T, H, D = q.shape
+        ws = torch.full((M.workspace_bytes(B, T, H, D),), 0xFF, dtype=torch.uint8, device=dev)
+        M.flashAttentionBackwardWorkspace(tg, to_gpu(Dv, dev), to_gpu(lse, dev), tq, tk, tv, dQ, dK, dV, ws)
+    else:
+        M.flashAttentionBackward(tg, to_gpu(Dv, dev), to_gpu(lse, dev), tq, tk, tv, dQ, dK, dV)
     return to_np(dQ), to_np(dK), to_np(dV)
 
 

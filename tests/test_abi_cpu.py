@@ -43,9 +43,13 @@ def test_invalid_shapes_rejected_without_device(change, code):
     assert lib.flashAttentionForward(fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
     assert lib.computeD(fake, fake, fake, ctypes.byref(p), None) == code
     assert lib.flashAttentionBackward(fake, fake, fake, fake, fake, fake, fake, fake, fake, ctypes.byref(p), None) == code
-    for part in (0, 1):
-        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+    for part in (0, 1, 2, 3):
+        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1 << 40,
                                             ctypes.byref(p), None) == code
+    assert lib.flashAttentionBackwardWorkspace(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1 << 40,
+                                               ctypes.byref(p), None) == code
+    n = ctypes.c_uint64()
+    assert lib.metalllmAttnBackwardWorkspaceSize(ctypes.byref(p), ctypes.byref(n)) == code
 
 
 def test_null_and_alignment_rejected():
@@ -55,6 +59,8 @@ def test_null_and_alignment_rejected():
     assert lib.flashAttentionForward(ok, ok, None, ok, ok, ctypes.byref(p), None) == -1
     assert lib.computeD(ok, None, ok, ctypes.byref(p), None) == -1
     assert lib.flashAttentionBackward(ok, ok, ok, ok, ok, ok, None, ok, ok, ctypes.byref(p), None) == -1
+    assert lib.flashAttentionBackwardWorkspace(ok, ok, ok, ok, ok, ok, None, ok, ok, ok, 1 << 40, ctypes.byref(p),
+                                               None) == -1
     assert lib.flashAttentionForward(ok, ok, ok, ok, ok, None, None) == -1
     bad = ctypes.c_void_p((1 << 20) + 2)
     assert lib.flashAttentionForward(ok, ok, bad, ok, ok, ctypes.byref(p), None) == -6
@@ -65,9 +71,36 @@ def test_backward_part_rejects_unknown_part():
     lib = M.library()
     p = AttentionParams(256, 384, 64, 6, 1)
     fake = ctypes.c_void_p(16)
-    for part in (-1, 2, 7):
-        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+    for part in (-1, 4, 7):
+        assert lib.metalllmAttnBackwardPart(part, fake, fake, fake, fake, fake, fake, fake, fake, fake, None, 0,
                                             ctypes.byref(p), None) == -4
+
+
+def test_workspace_size_and_validation():
+    """metalllmAttnBackwardWorkspaceSize is B*NH*(M/64)(M/64+1)/2 * 8192 bytes (64-bit, past 2^32 at
+    the target shape); the workspace entry point and parts 2/3 reject a NULL, misaligned or short
+    workspace before touching the device; parts 0/1 ignore it."""
+    lib = M.library()
+    n = ctypes.c_uint64()
+    for (B, T, H, D) in ((1, 64, 1, 64), (2, 192, 3, 128), (16, 4096, 16, 128), (128, 256, 6, 64)):
+        p = AttentionParams(T, H * D, D, H, B)
+        assert lib.metalllmAttnBackwardWorkspaceSize(ctypes.byref(p), ctypes.byref(n)) == 0
+        t = T // 64
+        assert n.value == B * H * t * (t + 1) // 2 * 8192
+    assert M.workspace_bytes(16, 4096, 16, 128) == 16 * 16 * 64 * 65 // 2 * 8192 > 1 << 32
+    p = AttentionParams(256, 384, 64, 6, 1)
+    assert lib.metalllmAttnBackwardWorkspaceSize(ctypes.byref(p), None) == -1
+    assert lib.metalllmAttnBackwardWorkspaceSize(ctypes.byref(p), ctypes.byref(n)) == 0
+    need = n.value
+    ok = ctypes.c_void_p(1 << 20)
+    args = [ok] * 9
+    f = lib.flashAttentionBackwardWorkspace
+    assert f(*args, None, need, ctypes.byref(p), None) == -1
+    assert f(*args, ctypes.c_void_p((1 << 20) + 8), need, ctypes.byref(p), None) == -6
+    assert f(*args, ok, need - 1, ctypes.byref(p), None) == -5
+    for part in (2, 3):
+        assert lib.metalllmAttnBackwardPart(part, *args, None, need, ctypes.byref(p), None) == -1
+        assert lib.metalllmAttnBackwardPart(part, *args, ok, need - 16, ctypes.byref(p), None) == -5
 
 
 def test_error_strings():

@@ -4,6 +4,9 @@ Bars: LSE within 1e-3; O within 1e-2 max-abs, except 
 bf16 spacing exceeds 1e-2 (|O| >= 2), where the bar is one bf16 ulp of the oracle's value;
 dQ/dK/dV within 2e-2 max-abs relative to max |grad|; computeD bit-exact (same inputs, same
 summation order); causal-mask and index logic exact (row 0 of O equals row 0 of V bit for bit).
+Both backward entry points are checked: flashAttentionBackward and flashAttentionBackwardWorkspace
+(the stored-dS path); their dK/dV must also be identical to each other, their dQ equal within
+1e-5 of max |dQ| (fp32 summation order).
 """
 import ctypes
 import os
@@ -38,12 +41,18 @@ def check_case(gpu, B, T, H, D, s, seed, b_end=0, threads=0):
     Dr = O.compute_d(sl(g), sl(out))
     assert np.array_equal(Dfull[:nb], Dr), f"computeD differs: {np.abs(Dfull[:nb] - Dr).max()}"
     # backward alone: both sides get the GPU's lse and D
-    dQ, dK, dV = gpu_backward(g, Dfull, lse, q, k, v, gpu)
     rQ, rK, rV = O.backward(sl(g), Dr, np.ascontiguousarray(lse[:nb]), sl(q), sl(k), sl(v), O.opts(threads=threads))
-    errs = {n: rel_to_max(x[:nb], r) for n, x, r in (("dQ", dQ, rQ), ("dK", dK, rK), ("dV", dV, rV))}
-    print("  bwd rel-to-max:", {n: f"{e:.3g}" for n, e in errs.items()}, flush=True)
-    for n, e in errs.items():
-        assert e <= 2e-2, n
+    res = []
+    for ws in (False, True):
+        dQ, dK, dV = gpu_backward(g, Dfull, lse, q, k, v, gpu, workspace=ws)
+        errs = {n: rel_to_max(x[:nb], r) for n, x, r in (("dQ", dQ, rQ), ("dK", dK, rK), ("dV", dV, rV))}
+        print(f"  bwd{' (workspace)' if ws else ''} rel-to-max:", {n: f"{e:.3g}" for n, e in errs.items()}, flush=True)
+        for n, e in errs.items():
+            assert e <= 2e-2, n
+        res.append((dQ, dK, dV))
+    (q0, k0, v0), (q1, k1, v1) = res
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    assert np.abs(q0 - q1).max() <= 1e-5 * np.abs(q0).max()
     return out, lse
 
 
@@ -84,8 +93,9 @@ def test_config3_slice(gpu):
 
 def test_config3_full_size_properties(gpu):
     """Config 3 at full size: row 0 of every head equals V row 0 bit for bit (causal index logic),
-    LSE finite, forward and dK/dV deterministic across runs, sum over keys of dV equal to the sum
-    over queries of dO (rows of P sum to 1)."""
+    LSE finite, forward and backward deterministic across runs, sum over keys of dV equal to the
+    sum over queries of dO (rows of P sum to 1); the workspace backward gives identical dK/dV and
+    dQ within fp32 summation order."""
     import torch
     import metalllm_amd as M
     B, T, H, D = 16, 4096, 16, 128
@@ -99,10 +109,15 @@ def test_config3_full_size_properties(gpu):
     assert torch.equal(out1, out2) and torch.equal(lse1, lse2)
     assert torch.equal(out1[:, 0], v[:, 0])
     assert torch.isfinite(lse1).all()
-    dQ1, dK1, dV1, _ = M.attention_backward(dO, q, k, v, out1, lse1)
+    dQ1, dK1, dV1, Dv = M.attention_backward(dO, q, k, v, out1, lse1)
     dQ2, dK2, dV2, _ = M.attention_backward(dO, q, k, v, out1, lse1)
-    assert torch.equal(dK1, dK2) and torch.equal(dV1, dV2)
-    assert (dQ1 - dQ2).abs().max().item() <= 1e-3 * dQ1.abs().max().item()  # atomic order only
+    assert torch.equal(dK1, dK2) and torch.equal(dV1, dV2) and torch.equal(dQ1, dQ2)
+    ws = torch.empty((M.workspace_bytes(B, T, H, D),), dtype=torch.uint8, device=dev)
+    dQ3, dK3, dV3 = torch.empty_like(dQ1), torch.empty_like(dK1), torch.empty_like(dV1)
+    M.flashAttentionBackwardWorkspace(dO, Dv, lse1, q, k, v, dQ3, dK3, dV3, ws)
+    assert torch.equal(dK1, dK3) and torch.equal(dV1, dV3)
+    assert (dQ1 - dQ3).abs().max().item() <= 1e-5 * dQ1.abs().max().item()
+    del ws
     sdv = dV1.float().sum(1)
     sdo = dO.float().sum(1)
     assert ((sdv - sdo).abs().max() / sdo.abs().max()).item() < 3e-2
@@ -142,29 +157,39 @@ def test_mfma_model_on_random_tiles(gpu):
     assert bad == 0, f"{bad} of {n * 1024} results differ from the model"
 
 
-def test_backward_overwrites_dk_dv_and_accumulates_dq(gpu):
-    """ABI contract: dK/dV are written in full (stale contents ignored); dQ is accumulated into."""
+def test_backward_writes_gradients_in_full(gpu):
+    """ABI contract: dQ, dK and dV are written in full (stale contents ignored: the result equals
+    the reference's accumulation into zeroed buffers), by both entry points, and a workspace's
+    stale contents do not matter either."""
     import torch
     import metalllm_amd as M
-    q, k, v, g = make_inputs(1, 256, 2, 64, 31)
-    tq, tk, tv, tg = (to_gpu(x, gpu) for x in (q, k, v, g))
-    out, lse = M.attention_forward(tq, tk, tv)
-    Dv = torch.empty((1, 2, 256), dtype=torch.float32, device=gpu)
-    M.computeD(tg, out, Dv)
-    dQ = torch.zeros((1, 256, 2, 64), dtype=torch.float32, device=gpu)
-    dK = torch.full_like(tq, 7.0)
-    dV = torch.full_like(tq, -3.0)
-    M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-    dQ2 = dQ.clone()
-    dK2, dV2 = dK.clone(), dV.clone()
-    M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-    assert torch.equal(dK, dK2) and torch.equal(dV, dV2)
-    assert (dQ - 2 * dQ2).abs().max().item() <= 1e-5 * dQ2.abs().max().item()
+    for T in (256, 192):
+        q, k, v, g = make_inputs(1, T, 2, 64, 31)
+        tq, tk, tv, tg = (to_gpu(x, gpu) for x in (q, k, v, g))
+        out, lse = M.attention_forward(tq, tk, tv)
+        Dv = torch.empty((1, 2, T), dtype=torch.float32, device=gpu)
+        M.computeD(tg, out, Dv)
+        ws = torch.full((M.workspace_bytes(1, T, 2, 64),), 0x7F, dtype=torch.uint8, device=gpu)
+        res = []
+        for fill in (0.0, 7.0, float("nan")):
+            for use_ws in (False, True):
+                dQ = torch.full((1, T, 2, 64), fill, dtype=torch.float32, device=gpu)
+                dK = torch.full_like(tq, fill)
+                dV = torch.full_like(tq, -fill)
+                if use_ws:
+                    M.flashAttentionBackwardWorkspace(tg, Dv, lse, tq, tk, tv, dQ, dK, dV, ws)
+                else:
+                    M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+                res.append((use_ws, dQ, dK, dV))
+        for use_ws, dQ, dK, dV in res:
+            ref = res[0] if not use_ws else res[1]
+            assert torch.isfinite(dQ).all() and torch.equal(dQ, ref[1])
+            assert torch.equal(dK, res[0][2]) and torch.equal(dV, res[0][3])
 
 
 def test_backward_parts_equal_flash_attention_backward(gpu):
-    """The bench hook: part 0 (dK/dV kernel) then part 1 (dQ kernel) is flashAttentionBackward, bit
-    for bit (one fp32 atomic per dQ element into a zeroed buffer, so the order does not matter)."""
+    """The bench hook: part 0 (dK/dV kernel) then part 1 (dQ kernel) is flashAttentionBackward, and
+    part 2 then part 3 is flashAttentionBackwardWorkspace, bit for bit."""
     import torch
     import metalllm_amd as M
     q, k, v, g = make_inputs(2, 512, 3, 128, 41)
@@ -172,16 +197,20 @@ def test_backward_parts_equal_flash_attention_backward(gpu):
     out, lse = M.attention_forward(tq, tk, tv)
     Dv = torch.empty((2, 3, 512), dtype=torch.float32, device=gpu)
     M.computeD(tg, out, Dv)
-    res = []
-    for split in (False, True):
-        dQ = torch.zeros((2, 512, 3, 128), dtype=torch.float32, device=gpu)
-        dK = torch.empty_like(tq)
-        dV = torch.empty_like(tq)
-        if split:
-            M.backward_part(0, tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-            M.backward_part(1, tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-        else:
-            M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-        res.append((dQ, dK, dV))
-    for a, b in zip(*res):
-        assert torch.equal(a, b)
+    ws = torch.empty((M.workspace_bytes(2, 512, 3, 128),), dtype=torch.uint8, device=gpu)
+    for first in (0, 2):
+        res = []
+        for split in (False, True):
+            dQ = torch.empty((2, 512, 3, 128), dtype=torch.float32, device=gpu)
+            dK = torch.empty_like(tq)
+            dV = torch.empty_like(tq)
+            if split:
+                M.backward_part(first, tg, Dv, lse, tq, tk, tv, dQ, dK, dV, workspace=ws)
+                M.backward_part(first + 1, tg, Dv, lse, tq, tk, tv, dQ, dK, dV, workspace=ws)
+            elif first == 0:
+                M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+            else:
+                M.flashAttentionBackwardWorkspace(tg, Dv, lse, tq, tk, tv, dQ, dK, dV, ws)
+            res.append((dQ, dK, dV))
+        for a, b in zip(*res):
+            assert torch.equal(a, b)
