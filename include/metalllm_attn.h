@@ -141,6 +141,38 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
  * count == 0 is a no-op; otherwise both pointers non-NULL and 16-byte aligned. */
 int castFloatToBfloat(const float* in, uint16_t* out, uint32_t count, metalllm_stream_t stream);
 
+/* elementwise.metal:7-17, model.h:368-376 (used at :483,618,695): out[i] = bf16(a[i] + b[i]) for
+ * i < count; out may alias a or b. The reference's buffer order (a0 b1 out2 count3). count == 0
+ * is a no-op; otherwise non-NULL 16-byte aligned pointers. */
+int residualAdd(const uint16_t* a, const uint16_t* b, uint16_t* out, uint32_t count, metalllm_stream_t stream);
+
+/* layernorm.metal:3-8 / main.cpp:89-96: {rows, cols, group_size, eps}. group_size (the reference's
+ * threads per row) is not used here: one wave handles a row. */
+typedef struct LayernormParams {
+  uint32_t rows;
+  uint32_t cols;       /* a multiple of 8, at most 4096 */
+  uint32_t group_size;
+  float eps;           /* the reference's default is 1e-5 */
+} LayernormParams;
+
+/* layernorm.metal:10-70, dispatched by encodeLayernormForward (model.h:385-396). Per row of x
+ * (bf16 [rows, cols]): mean and variance in fp32, stdev[row] = sqrt(var + eps) (fp32),
+ * x_norm = bf16((x - mean) / stdev), out = bf16(gamma * x_norm_fp32 + beta) (gamma, beta bf16
+ * [cols]). Buffer order x0 x_norm1 out2 gamma3 beta4 stdev5 params6. */
+int layernormForward(const uint16_t* x, uint16_t* x_norm, uint16_t* out, const uint16_t* gamma, const uint16_t* beta,
+                     float* stdev, const LayernormParams* p, metalllm_stream_t stream);
+
+/* layernorm.metal:73-127, dispatched by encodeLayernormBackward (model.h:398-410). In place on dZ
+ * (bf16 [rows, cols]): dgamma[c] += sum_rows bf16(x_norm*dZ), dbeta[c] += sum_rows dZ (fp32
+ * [cols], accumulated: the caller zeroes them, model.h:543-548); dx_norm = bf16(dZ*gamma) is
+ * written when dx_norm is non-NULL (the reference's scratch, model.h's dXnormBuffer); then
+ * dZ = bf16((dx_norm - mean(dx_norm) - x_norm*mean(bf16(dx_norm*x_norm))) / stdev). Buffer order
+ * dZ0 x_norm_cache1 gamma2 stdev3 dx_norm5 dgamma6 dbeta7 params8 (the reference binds nothing
+ * at index 4). */
+int layernormBackward(uint16_t* dZ, const uint16_t* x_norm_cache, const uint16_t* gamma, const float* stdev,
+                      uint16_t* dx_norm, float* dgamma, float* dbeta, const LayernormParams* p,
+                      metalllm_stream_t stream);
+
 /* ---- Phase encoder (model.h:441-508 forward, :538-708 backward: one command buffer per phase) ----
  * The attention sublayer's buffers, as model.h's BlockBuffers hold them (model.h:236-277). All
  * device pointers, 16-byte aligned; shapes from AttentionParams as above (R = B*M rows, N = C

@@ -7,8 +7,9 @@ from .attention import (AttentionError, AttentionParams, attention_backward, att
                         computeD, flashAttentionBackward, flashAttentionBackwardWorkspace, flashAttentionForward,
                         library, work_map, workspace_bytes)
 
+from . import glue  # noqa: E402  (layernorm, residual add, dX cast around the sublayer)
 from . import sublayer  # noqa: E402  (the GEMMs around the attention core)
 
-__all__ = ["sublayer", "AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
+__all__ = ["glue", "sublayer", "AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
            "computeD", "flashAttentionBackward", "flashAttentionBackwardWorkspace", "flashAttentionForward", "library",
            "work_map", "workspace_bytes"]

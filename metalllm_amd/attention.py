@@ -27,7 +27,8 @@ ERRORS = {
 EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
             "metalllmAttnErrorString", "metalllmAttnWorkMap", "computeQKV", "projForward", "projBackwarddW",
             "projBackwarddX", "computeGradDx", "computeGradDw", "castFloatToBfloat", "metalllmSublayerEncode",
-            "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize",
+            "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize", "residualAdd",
+            "layernormForward", "layernormBackward",
             "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy")
 
 

@@ -16,6 +16,7 @@ import ctypes
 
 from .attention import (AttentionParams, _check, _lib, _ptr, _stream, backward_part, computeD, flashAttentionForward,
                         workspace_bytes)
+from .glue import castFloatToBfloat  # noqa: F401  (the dX handoff, model.h:692)
 
 _BOUND = False
 
@@ -32,14 +33,13 @@ def _L():
         L.projBackwarddX.argtypes = [vp] * 3 + [pp, vp]
         L.computeGradDx.argtypes = [vp] * 7 + [pp, vp]
         L.computeGradDw.argtypes = [vp] * 7 + [pp, vp]
-        L.castFloatToBfloat.argtypes = [vp, vp, ctypes.c_uint32, vp]
         bp = ctypes.POINTER(SublayerBuffers)
         L.metalllmSublayerEncode.argtypes = [ctypes.c_int, bp, pp, vp]
         L.metalllmSublayerGraphCreate.argtypes = [ctypes.c_int, bp, pp, ctypes.POINTER(vp)]
         L.metalllmSublayerGraphLaunch.argtypes = [vp, vp]
         L.metalllmSublayerGraphDestroy.argtypes = [vp]
         for f in (L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw,
-                  L.castFloatToBfloat, L.metalllmSublayerEncode, L.metalllmSublayerGraphCreate,
+                  L.metalllmSublayerEncode, L.metalllmSublayerGraphCreate,
                   L.metalllmSublayerGraphLaunch, L.metalllmSublayerGraphDestroy):
             f.restype = ctypes.c_int
         _BOUND = True
@@ -96,12 +96,6 @@ def computeGradDw(x, dQ, dK, dV, dQw, dKw, dVw, p: AttentionParams, stream=None)
     """attention.metal:343-383: dQw += x^T.dQ (fp32); dKw, dVw += x^T.dK, x^T.dV (bf16); accumulated."""
     _check(_L().computeGradDw(_ptr(x), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dQw), _ptr(dKw), _ptr(dVw),
                               ctypes.byref(p), _stream(stream)), "computeGradDw")
-
-
-def castFloatToBfloat(inp, out, count=None, stream=None):
-    """elementwise.metal:19-28: out[i] = bf16(in[i]) (round to nearest even) for i < count."""
-    n = inp.numel() if count is None else count
-    _check(_L().castFloatToBfloat(_ptr(inp), _ptr(out), n, _stream(stream)), "castFloatToBfloat")
 
 
 def encode_phase(phase: int, bufs: SublayerBuffers, p: AttentionParams, stream=None):

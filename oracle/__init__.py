@@ -182,6 +182,61 @@ def castFloatToBfloat(x: np.ndarray) -> np.ndarray:
     return r.astype(np.uint16)
 
 
+def _bf_round(x: np.ndarray) -> np.ndarray:
+    """fp32 -> nearest bf16 value, as fp32 (a bfloat result of Metal bfloat arithmetic)."""
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, dtype=np.float32)))
+
+
+def _sum32(x: np.ndarray, axis: int) -> np.ndarray:
+    """An fp32 reduction, modelled order-independently: the exact sum of the fp32 terms rounded once
+    to fp32 (the reference's simd_sum/threadgroup order is not specified; any order lies within the
+    fp32 summation bound of this value)."""
+    return np.asarray(x, dtype=np.float32).astype(np.float64).sum(axis=axis).astype(np.float32)
+
+
+def residualAdd(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """elementwise.metal:7-17: out = bfloat(float(a) + float(b)) (fp32 add, one rounding)."""
+    return castFloatToBfloat(bf16_to_f32(a) + bf16_to_f32(b))
+
+
+def layernormForward(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-5):
+    """layernorm.metal:10-70, rows of x (bf16 bits [rows, cols]); returns (x_norm bf16, out bf16,
+    stdev fp32 [rows]). fp32 arithmetic in the reference's order: mean = sum/cols, var =
+    sum((x - mean)^2)/cols, std = sqrt(var + eps), rstd = 1/std, xn = (x - mean)*rstd,
+    out = gamma*xn + beta (multiply and add rounded separately)."""
+    xf = bf16_to_f32(x)
+    cols = np.float32(xf.shape[1])
+    mean = (_sum32(xf, 1) / cols).astype(np.float32)
+    d = (xf - mean[:, None]).astype(np.float32)
+    var = (_sum32((d * d).astype(np.float32), 1) / cols).astype(np.float32)
+    sd = np.sqrt((var + np.float32(eps)).astype(np.float32)).astype(np.float32)
+    rstd = (np.float32(1.0) / sd).astype(np.float32)
+    xn = (d * rstd[:, None]).astype(np.float32)
+    out = ((bf16_to_f32(gamma)[None, :] * xn).astype(np.float32) + bf16_to_f32(beta)[None, :]).astype(np.float32)
+    return f32_to_bf16(xn), f32_to_bf16(out), sd
+
+
+def layernormBackward(dZ: np.ndarray, x_norm: np.ndarray, gamma: np.ndarray, stdev: np.ndarray,
+                      dgamma: np.ndarray, dbeta: np.ndarray):
+    """layernorm.metal:73-127; returns (new dZ bf16, dx_norm bf16, dgamma fp32, dbeta fp32), the
+    column sums added to the given dgamma/dbeta. bfloat*bfloat products are rounded to bf16
+    (Metal's bfloat arithmetic): g = bf16(xn*dZ), dxn = bf16(dZ*gamma), the sum2 terms
+    bf16(dxn*xn); then dZ = bf16(rdev*((dxn - sum1/cols) - xn*(sum2/cols))) with rdev = 1/stdev."""
+    z = bf16_to_f32(dZ)
+    x = bf16_to_f32(x_norm)
+    g = bf16_to_f32(gamma)
+    cols = np.float32(z.shape[1])
+    dg = (np.asarray(dgamma, np.float32).astype(np.float64) + _bf_round(x * z).astype(np.float64).sum(0))
+    db = (np.asarray(dbeta, np.float32).astype(np.float64) + z.astype(np.float64).sum(0))
+    dxn = _bf_round(z * g[None, :])
+    rs1 = (_sum32(dxn, 1) / cols).astype(np.float32)
+    rs2 = (_sum32(_bf_round(dxn * x), 1) / cols).astype(np.float32)
+    rdev = (np.float32(1.0) / np.asarray(stdev, np.float32)).astype(np.float32)
+    t = ((dxn - rs1[:, None]).astype(np.float32) - (x * rs2[:, None]).astype(np.float32)).astype(np.float32)
+    out = (rdev[:, None] * t).astype(np.float32)
+    return f32_to_bf16(out), f32_to_bf16(dxn), dg.astype(np.float32), db.astype(np.float32)
+
+
 # ---- sublayer GEMMs (gemm_oracle.cpp): row-major, R = B*T rows, C = NH*D features ----
 T_BF16, T_F32 = 0, 1
 _GEMM_BOUND = False

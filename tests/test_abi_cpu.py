@@ -196,3 +196,28 @@ def test_phase_encoder_validates_before_device(entry):
         assert out.value is None
         assert lib.metalllmSublayerGraphLaunch(None, None) == -1
         assert lib.metalllmSublayerGraphDestroy(None) == 0
+
+
+def test_glue_entry_points_validate_before_device():
+    """residualAdd and the layernorm kernels reject bad parameters, NULL and misaligned pointers
+    without a device call."""
+    from metalllm_amd.glue import LayernormParams, _L
+    lib = _L()
+    ok = ctypes.c_void_p(1 << 20)
+    mis = ctypes.c_void_p((1 << 20) + 2)
+    assert lib.residualAdd(None, None, None, 0, None) == 0
+    assert lib.residualAdd(ok, None, ok, 8, None) == -1
+    assert lib.residualAdd(ok, ok, mis, 8, None) == -6
+    good = LayernormParams.of(64, 768)
+    for bad, code in ((LayernormParams.of(0, 768), -4), (LayernormParams.of(64, 0), -4),
+                      (LayernormParams.of(64, 100), -4), (LayernormParams.of(64, 4104), -4),
+                      (LayernormParams(64, 768, 768, float("nan")), -4), (LayernormParams(64, 768, 768, -1.0), -4),
+                      (LayernormParams.of(1 << 20, 4096), -5)):
+        assert lib.layernormForward(ok, ok, ok, ok, ok, ok, ctypes.byref(bad), None) == code
+        assert lib.layernormBackward(ok, ok, ok, ok, ok, ok, ok, ctypes.byref(bad), None) == code
+    assert lib.layernormForward(ok, ok, ok, ok, ok, ok, None, None) == -1
+    assert lib.layernormForward(ok, None, ok, ok, ok, ok, ctypes.byref(good), None) == -1
+    assert lib.layernormForward(ok, ok, ok, mis, ok, ok, ctypes.byref(good), None) == -6
+    assert lib.layernormBackward(ok, ok, ok, ok, ok, None, ok, ctypes.byref(good), None) == -1
+    assert lib.layernormBackward(ok, ok, ok, ok, mis, ok, ok, ctypes.byref(good), None) == -6  # dx_norm, when given
+    assert ctypes.sizeof(LayernormParams) == 16
