@@ -201,6 +201,20 @@ typedef struct metalllmSublayerBuffers {
   uint16_t* dVw;
   uint16_t* dProjw;
   uint16_t* dX_bf16;      /* optional (NULL: skipped): bf16(dX), model.h:692                   */
+  /* Optional: the rest of the block's attention half (model.h:445 ln1, :483 and :695 residual
+   * adds, :692-694 cast and ln1 backward). All NULL: the sublayer alone. When `hidden` is set,
+   * every field below must be, X becomes an output (phase 0 writes ln1(hidden) into it) and
+   * dX_bf16 is ignored (phase 1 casts dX into dStream). */
+  const uint16_t* hidden;   /* bf16 [R, N]: the block input                                    */
+  const uint16_t* ln_gamma; /* bf16 [N]                                                         */
+  const uint16_t* ln_beta;  /* bf16 [N]                                                         */
+  uint16_t* ln_xnorm;       /* bf16 [R, N]: ln1's x_norm cache                                  */
+  float* ln_stdev;          /* fp32 [R]                                                         */
+  float* ln_dgamma;         /* fp32 [N], zeroed by phase 1 (model.h:543-544)                    */
+  float* ln_dbeta;          /* fp32 [N]                                                         */
+  uint16_t* residual;       /* bf16 [R, N]: phase 0 output hidden + out (model.h's residual1)   */
+  uint16_t* dStream;        /* bf16 [R, N]: phase 1 output, the gradient at hidden              */
+  float ln_eps;             /* ln1's eps (the reference's default is 1e-5)                      */
 } metalllmSublayerBuffers;
 
 typedef struct metalllmSublayerGraph metalllmSublayerGraph;
@@ -211,6 +225,9 @@ typedef struct metalllmSublayerGraph metalllmSublayerGraph;
  *            projBackwarddX, computeD, flashAttentionBackwardWorkspace, computeGradDx,
  *            computeGradDw (one two-term split of dQ serves both), and castFloatToBfloat(dX) when
  *            dX_bf16 is set.
+ * With the block fields set: phase 0 starts with layernormForward(hidden -> X) and ends with
+ * residualAdd(hidden, out -> residual); phase 1 also zeroes ln_dgamma/ln_dbeta, casts dX into
+ * dStream, then runs layernormBackward(dStream) and residualAdd(dStream, dOut -> dStream).
  * Validation: the GEMM rules and the attention rules above, every pointer the phase uses.
  * Uses the device's shared rocBLAS handle and scratch like the GEMM entry points above (plus a
  * per-device attention workspace, metalllmAttnBackwardWorkspaceSize bytes, grown on demand). */

@@ -407,6 +407,11 @@ int check_phase(int phase, const metalllmSublayerBuffers* b, const AttentionPara
                b->Dsum, b->dQ, b->dK, b->dV, b->dX, b->dQw, b->dKw, b->dVw, b->dProjw);
     if (b->dX_bf16 && !aligned16(b->dX_bf16)) return METALLLM_ATTN_E_ALIGN;
   }
+  if (b->hidden) {  // the block's attention half
+    CHECK_PTRS(b->hidden, b->ln_gamma, b->ln_beta, b->ln_xnorm, b->ln_stdev, b->ln_dgamma, b->ln_dbeta, b->residual,
+               b->dStream);
+    if (p->N > 4096 || !(b->ln_eps >= 0.0f)) return METALLLM_ATTN_E_LAYOUT;
+  }
   return METALLLM_ATTN_OK;
 }
 
@@ -416,10 +421,20 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   const int R = (int)(p->B * p->M), C = (int)p->N;
   const size_t e = (size_t)R * C;
   const metalllm_stream_t s = (metalllm_stream_t)c.stream;
+  const bool block = b->hidden != nullptr;
+  const LayernormParams lp{(uint32_t)R, (uint32_t)C, (uint32_t)std::min(C, 1024), b->ln_eps};
   if (phase == 0) {
+    if (block && !c.query)  // model.h:445: X = ln1(hidden)
+      TRY(layernormForward(b->hidden, b->ln_xnorm, (uint16_t*)b->X, b->ln_gamma, b->ln_beta, b->ln_stdev, &lp, s));
     TRY(op_qkv(c, b->X, b->q, b->k, b->v, b->q_w, b->k_w, b->v_w, R, C));
     if (!c.query) TRY(flashAttentionForward(b->q, b->k, b->v, b->attn_out, b->l, p, s));
-    return op_proj_fwd(c, b->attn_out, b->proj_w, b->out, R, C);
+    TRY(op_proj_fwd(c, b->attn_out, b->proj_w, b->out, R, C));
+    if (block && !c.query) TRY(residualAdd(b->hidden, b->out, b->residual, (uint32_t)e, s));  // model.h:483
+    return METALLLM_ATTN_OK;
+  }
+  if (block) {  // model.h:545-546
+    TRY(zero_bytes(c, b->ln_dgamma, (size_t)C * 4));
+    TRY(zero_bytes(c, b->ln_dbeta, (size_t)C * 4));
   }
   // model.h:549-555 zeroes the accumulated gradients before the pass (the attention backward
   // writes dQ, dK and dV in full)
@@ -438,7 +453,14 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
   TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, split, split + e, b->dK, b->dV, R, C));
   TRY(op_grad_dw(c, b->X, split, split + e, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
-  if (b->dX_bf16 && !c.query) TRY(castFloatToBfloat(b->dX, b->dX_bf16, (uint32_t)e, s));
+  if (c.query) return METALLLM_ATTN_OK;
+  if (block) {  // model.h:692-695
+    TRY(castFloatToBfloat(b->dX, b->dStream, (uint32_t)e, s));
+    TRY(layernormBackward(b->dStream, b->ln_xnorm, b->ln_gamma, b->ln_stdev, nullptr, b->ln_dgamma, b->ln_dbeta, &lp,
+                          s));
+    return residualAdd(b->dStream, b->dOut, b->dStream, (uint32_t)e, s);
+  }
+  if (b->dX_bf16) TRY(castFloatToBfloat(b->dX, b->dX_bf16, (uint32_t)e, s));
   return METALLLM_ATTN_OK;
 }
 

@@ -50,8 +50,9 @@ class SublayerBuffers(ctypes.Structure):
     """metalllmSublayerBuffers: the sublayer's device buffers (model.h:236-277), field order as in
     include/metalllm_attn.h."""
     FIELDS = ("X", "q_w", "k_w", "v_w", "proj_w", "q", "k", "v", "attn_out", "l", "out", "dOut", "dAttn", "Dsum", "dQ",
-              "dK", "dV", "dX", "dQw", "dKw", "dVw", "dProjw", "dX_bf16")
-    _fields_ = [(n, ctypes.c_void_p) for n in FIELDS]
+              "dK", "dV", "dX", "dQw", "dKw", "dVw", "dProjw", "dX_bf16", "hidden", "ln_gamma", "ln_beta", "ln_xnorm",
+              "ln_stdev", "ln_dgamma", "ln_dbeta", "residual", "dStream")
+    _fields_ = [(n, ctypes.c_void_p) for n in FIELDS] + [("ln_eps", ctypes.c_float)]
 
 
 def params_of(x, H: int) -> AttentionParams:
@@ -137,8 +138,12 @@ class Sublayer:
     flashAttentionBackward, computeGradDx, computeGradDw (model.h:621-690), with the gradient
     buffers zeroed first as model.h:549-555 does."""
 
-    def __init__(self, X, Wq, Wk, Wv, Wp, H: int):
+    def __init__(self, X, Wq, Wk, Wv, Wp, H: int, hidden=None, ln_gamma=None, ln_beta=None, ln_eps: float = 1e-5):
+        """X: the sublayer input [B, T, C]. With `hidden` (and ln_gamma, ln_beta) the phase encoder
+        runs the block's attention half: X is then allocated here and written by ln1(hidden)."""
         import torch
+        if hidden is not None:
+            X = torch.empty_like(hidden)
         self.X, self.Wq, self.Wk, self.Wv, self.Wp, self.H = X, Wq, Wk, Wv, Wp, H
         B, T, C = X.shape
         self.p = params_of(X, H)
@@ -160,6 +165,12 @@ class Sublayer:
         self.dXb = bf()       # bf16(dX), the handoff to the layernorm backward (model.h:692)
         self.D = D
         self.graphs = None
+        self.hidden, self.ln_gamma, self.ln_beta, self.ln_eps = hidden, ln_gamma, ln_beta, ln_eps
+        if hidden is not None:
+            self.ln_xnorm, self.residual, self.dStream = bf(), bf(), bf()
+            self.ln_stdev = torch.empty((B * T,), dtype=torch.float32, device=dev)
+            self.ln_dgamma = torch.empty((C,), dtype=torch.float32, device=dev)
+            self.ln_dbeta = torch.empty((C,), dtype=torch.float32, device=dev)
 
     def buffers(self, cast: bool = True) -> SublayerBuffers:
         """The struct of device pointers; cast=False leaves dX_bf16 NULL (no dX handoff)."""
@@ -170,8 +181,12 @@ class Sublayer:
                  dX_bf16=self.dXb)
         if not cast:
             t["dX_bf16"] = None
+        blk = ("hidden", "ln_gamma", "ln_beta", "ln_xnorm", "ln_stdev", "ln_dgamma", "ln_dbeta", "residual", "dStream")
+        for n in blk:
+            t[n] = getattr(self, n) if self.hidden is not None else None
         for n in SublayerBuffers.FIELDS:
             setattr(b, n, _ptr(t[n]).value if t[n] is not None else None)
+        b.ln_eps = self.ln_eps
         return b
 
     def encode(self, phase: int, stream=None):

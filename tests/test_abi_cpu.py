@@ -154,6 +154,7 @@ def test_sublayer_buffers_struct_matches_header():
     body = text[text.index("typedef struct metalllmSublayerBuffers {"):text.index("} metalllmSublayerBuffers;")]
     names = re.findall(r"\*\s*(\w+);", body)
     assert tuple(names) == SublayerBuffers.FIELDS
+    assert re.findall(r"float (\w+);", body) == ["ln_eps"] and SublayerBuffers._fields_[-1][0] == "ln_eps"
 
 
 @pytest.mark.parametrize("entry", ["metalllmSublayerEncode", "metalllmSublayerGraphCreate"])
@@ -191,6 +192,21 @@ def test_phase_encoder_validates_before_device(entry):
     b = SublayerBuffers(*[getattr(full, n) for n in SublayerBuffers.FIELDS])
     b.dX_bf16 = full.dX_bf16 + 2  # optional, but aligned when given
     assert call(1, b, P()) == -6
+    # the block fields: all or none once `hidden` is set; N <= 4096 for the layernorm; eps >= 0
+    blk = ("ln_gamma", "ln_beta", "ln_xnorm", "ln_stdev", "ln_dgamma", "ln_dbeta", "residual", "dStream")
+    for phase in (0, 1):
+        b = SublayerBuffers(*[getattr(full, n) for n in SublayerBuffers.FIELDS], 1e-5)
+        for name in blk:
+            setattr(b, name, None)
+        b.hidden = full.hidden
+        assert call(phase, b, P()) == -1
+        for name in blk:
+            setattr(b, name, getattr(full, name))
+        b.ln_eps = -1.0
+        assert call(phase, b, P()) == -4
+        b.ln_eps = 1e-5
+        b.residual = full.residual + 8
+        assert call(phase, b, P()) == -6
     if entry.endswith("Create"):
         assert lib.metalllmSublayerGraphCreate(0, ctypes.byref(full), ctypes.byref(P()), None) == -1
         assert out.value is None

@@ -4,8 +4,9 @@ command buffers, :441-508 and :538-708, as launch sequences and HIP graphs).
 
 Bars: the cast is bit-exact against the oracle. The encoder runs the same kernels on the same
 inputs as the per-call chain (whose stages test_gpu_sublayer.py checks against the oracle), so its
-results must be bit-identical to that chain; every kernel on the path is deterministic (dQ gets
-one fp32 add per element into a zeroed buffer). Graph replays must be bit-identical to the eager
+results must be bit-identical to that chain; every kernel on the path is deterministic (each
+gradient element has one writer; only the layernorm's dgamma/dbeta column sums use atomics, and
+they are compared within fp32 summation order). Graph replays must be bit-identical to the eager
 encoder on the same inputs, replay after replay, with eager work and new inputs in between.
 """
 import numpy as np
@@ -114,3 +115,62 @@ def test_graph_replays_match_encoder(gpu, S):
                 assert np.array_equal(rg[n], re[n]), (B, T, H, C, it, n)
             print(f"shape {(B, T, H, C)} replay {it}: identical to the encoder")
         g.close()
+
+
+def test_block_half_encoder_and_graphs(gpu, S):
+    """The block's attention half (ln1, sublayer, residual add; backward with the dX cast, ln1
+    backward and the skip add) through the encoder and as graphs equals the same sequence issued
+    through the public entry points (model.h:445-483, 617-695), bit for bit."""
+    import torch
+    import metalllm_amd.glue as G
+    B, T, H, C = 2, 256, 6, 384
+    rng = np.random.default_rng(41)
+    bfg = lambda shape, sc=1.0, sh=0.0: to_gpu(O.f32_to_bf16((rng.standard_normal(shape) * sc + sh).astype(np.float32)), gpu)
+    hidden = bfg((B, T, C), 1.0, 0.3)
+    gamma, beta = bfg((C,), 0.1, 1.0), bfg((C,), 0.1)
+    Ws = [bfg((C, C), 0.02) for _ in range(4)]
+    dOut = bfg((B, T, C))
+    blk = S.Sublayer(None, *Ws, H=H, hidden=hidden, ln_gamma=gamma, ln_beta=beta)
+    blk.dOut.copy_(dOut)
+    blk.encode(0)
+    blk.encode(1)
+    # the same sequence through the public calls
+    ref = S.Sublayer(torch.empty_like(hidden), *Ws, H=H)
+    xnorm, stdev = torch.empty_like(hidden), torch.empty(B * T, dtype=torch.float32, device=gpu)
+    G.layernormForward(hidden, xnorm, ref.X, gamma, beta, stdev)
+    ref.forward()
+    residual = torch.empty_like(hidden)
+    G.residualAdd(hidden, ref.out, residual)
+    ref.zero_grads()
+    ref.backward(dOut)
+    dStream = torch.empty_like(hidden)
+    G.castFloatToBfloat(ref.dX, dStream)
+    dg = torch.zeros(C, dtype=torch.float32, device=gpu)
+    db = torch.zeros(C, dtype=torch.float32, device=gpu)
+    G.layernormBackward(dStream, xnorm, gamma, stdev, dg, db)
+    G.residualAdd(dStream, dOut, dStream)
+    torch.cuda.synchronize()
+    pairs = [("X", blk.X, ref.X), ("xnorm", blk.ln_xnorm, xnorm), ("stdev", blk.ln_stdev, stdev),
+             ("out", blk.out, ref.out), ("residual", blk.residual, residual), ("dX", blk.dX, ref.dX),
+             ("dWq", blk.dWq, ref.dWq), ("dWp", blk.dWp, ref.dWp), ("dStream", blk.dStream, dStream)]
+    for name, a, b in pairs:
+        assert torch.equal(a, b), name
+    # dgamma/dbeta: fp32 column sums added with atomics (order varies between runs)
+    for name, a, b in (("dgamma", blk.ln_dgamma, dg), ("dbeta", blk.ln_dbeta, db)):
+        assert (a - b).abs().max().item() <= 1e-5 * b.abs().max().item(), name
+    # graphs of both phases on new block inputs, against the encoder
+    snap = lambda: [t.clone() for _, t, _ in pairs]
+    blk.capture()
+    for it in range(2):
+        hidden.copy_(bfg((B, T, C), 1.0, 0.3))
+        blk.dOut.copy_(bfg((B, T, C)))
+        blk.replay(0)
+        blk.replay(1)
+        torch.cuda.synchronize()
+        got = snap()
+        blk.encode(0)
+        blk.encode(1)
+        torch.cuda.synchronize()
+        for (name, t, _), g in zip(pairs, got):
+            assert torch.equal(t, g), (it, name)
+    blk.close()
