@@ -23,6 +23,9 @@
 // Both matrix-core operands come from LDS by ds_read_b64_tr_b16: A = K^T (m = d, k = key),
 // B = dS^T (k = key, n = query position). dQ goes back through LDS ([q][d] fp32) so that its
 // stores are row-contiguous; every row of dQ is written once, in full.
+#include <algorithm>
+#include <atomic>
+
 #include "attn_common.hpp"
 #include "attn_launch.hpp"
 
@@ -175,9 +178,191 @@ __global__ void __launch_bounds__(256, 2) dqs_kernel(BwdArgs a) {
   }
 }
 
+// Persistent form of dqs_kernel (same work split, operands and results), used when the pair
+// count is a multiple of 8: a grid of two workgroups per CU, where the workgroups on XCD x serve
+// the pairs p = x (mod 8), so each pair's K tiles stay in one L2. That XCD's (pair, query block)
+// items are listed pair by pair, each pair's blocks largest first, and dealt in snake order
+// across its workgroups. Workgroups working at the same time then share one or two pairs'
+// K tiles, and every workgroup gets about the same number of key tiles (a large block in one row
+// of the deal meets a small one in the next). Stages
+// run back to back across item boundaries: the first stage of the next item is copied while the
+// last one of the current item is computed, and the item's dQ is stored straight from the
+// accumulators (16-byte stores, row segments that L2 merges into whole lines), those stores
+// completing while the next item's first stage is computed.
+template <int D>
+__global__ void __launch_bounds__(256, 2) dqs_persistent_kernel(BwdArgs a) {
+  using C = DqsCfg<D>;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::NSTAGE * C::STAGE];
+  constexpr int NSTORE = C::MB * 2 * 4;  // dQ store instructions per wave per item
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31, g16 = lane >> 4, s16 = lane & 15;
+  const int nqt = a.T / 64;
+  const int nqb = (nqt + C::QT - 1) / C::QT;
+  const int P8 = a.B * a.H / 8;                         // pairs per XCD
+  const int x = blockIdx.x & 7, w = blockIdx.x >> 3, Wx = gridDim.x >> 3;
+  const int nlist = P8 * nqb;                           // items on this XCD
+  const int rs = a.H * D;
+  const int wq = wave >> 1, wd = wave & 1;
+  const size_t ntri = (size_t)nqt * (nqt + 1) / 2;
+
+  // item k of this workgroup -> list index (snake order) -> (pair, query block)
+  auto list_index = [&](int k) { return k * Wx + ((k & 1) ? Wx - 1 - w : w); };
+  struct Item {
+    int pair, qt0, nk;
+  };
+  auto item_at = [&](int m) -> Item {
+    const int j = m / nqb, local = m - j * nqb;
+    const int qblk = nqb - 1 - local;
+    const int qt0 = C::QT * qblk;
+    return Item{8 * j + x, qt0, min(qt0 + C::QT, nqt)};
+  };
+  auto base_of = [&](int pair) -> size_t {
+    const int b = pair / a.H, hd = pair - b * a.H;
+    return ((size_t)b * a.T * a.H + hd) * D;
+  };
+
+  uint32_t koff[C::KPW], kdst[C::KPW];
+#pragma unroll
+  for (int j = 0; j < C::KPW; ++j) {
+    const int ins = wave + 4 * j < C::SLOTS ? wave + 4 * j : wave;
+    const int s = 64 * ins + lane, row = s / C::SLOTS, c = min(s % C::SLOTS, D / 8 - 1);
+    koff[j] = (uint32_t)(row * rs * 2 + c * 16);
+    kdst[j] = 1024u * ins;
+  }
+  const uint32_t smem_a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
+  auto issue = [&](const Item& it, int kt, int stage) {
+    const uint32_t dst = smem_a + stage * C::STAGE;
+    const char* ks = (const char*)(a.k + base_of(it.pair)) + (size_t)kt * 64 * rs * 2;
+#pragma unroll
+    for (int j = 0; j < C::KPW; ++j) dma16(koff[j], ks, dst + kdst[j]);
+    const char* dsg = (const char*)a.dS + (size_t)it.pair * ntri * 8192;
+#pragma unroll
+    for (int j = 0; j < 2 * C::QT; ++j) {
+      const int ins = wave + 4 * j, t = ins >> 3, row = ins & 7;
+      const int qt = it.qt0 + t;
+      const bool valid = qt < nqt && kt <= qt;
+      const char* src = dsg + (valid ? ((size_t)qt * (qt + 1) / 2 + kt) * 8192 : 0);
+      dma16_nt((uint32_t)(lane * 16 + row * 1024), src, dst + C::KBYTES + t * C::DSBYTES + row * C::SBLK);
+    }
+  };
+
+  const uint32_t a_lane =
+      2 * ((8 * (g16 >> 1) + (s16 >> 2)) * C::KP + 16 * (g16 & 1) + 4 * (s16 & 3)) + wd * D;
+  const uint32_t b_lane = C::KBYTES + wq * C::DSBYTES + (2 * (g16 & 1) + ((s16 & 3) >> 1)) * C::SBLK +
+                          (8 * (g16 >> 1) + (s16 >> 2)) * 16 + 8 * (s16 & 1);
+
+  f32x16 acc[C::MB][2];
+#pragma unroll
+  for (int m = 0; m < C::MB; ++m) acc[m][0] = acc[m][1] = zero16();
+
+  auto compute = [&](int stage) {
+    const uint32_t sa = smem_a + stage * C::STAGE;
+    const uint32_t ab = sa + a_lane, bb = sa + b_lane;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 Bo[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const uint32_t bd = bb + 4 * (ks >> 1) * C::SBLK + (16 * (ks & 1) + 32 * nb) * 16;
+        const u32x2 lo = tr_at(bd), hi = tr_at(bd + 4 * 16);
+        Bo[nb] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+#pragma unroll
+      for (int m = 0; m < C::MB; ++m) {
+        const uint32_t ad = ab + 2 * (16 * ks * C::KP + 32 * m);
+        const u32x2 lo = tr_at(ad), hi = tr_at(ad + 2 * 4 * C::KP);
+        const u32x4 A = u32x4{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[m][nb] = mfma(A, Bo[nb], acc[m][nb]);
+      }
+    }
+  };
+
+  int k = 0, m = list_index(0);
+  if (m >= nlist) return;  // more workgroups than items on this XCD
+  Item cur = item_at(m);
+  // the next stage to copy: item kn at key tile ktn
+  int kn = 0, ktn = 0;
+  Item nxt = cur;
+  bool have_next = true;
+  auto advance_next = [&]() {
+    if (++ktn == nxt.nk) {
+      ktn = 0;
+      const int mn = list_index(++kn);
+      have_next = mn < nlist;
+      if (have_next) nxt = item_at(mn);
+    }
+  };
+  issue(nxt, ktn, 0);
+  advance_next();
+  bool stored = false;  // this wave's dQ stores were issued after the copies now awaited
+  int kt = 0;
+  for (int t = 0;; ++t) {
+    if (stored)
+      wait_vm<NSTORE>();  // the copies of stage t landed; the previous item's stores may be in flight
+    else
+      wait_vm<0>();
+    __syncthreads();
+    if (have_next) {
+      issue(nxt, ktn, (t + 1) & 1);
+      advance_next();
+    }
+    const int qtw = cur.qt0 + wq;
+    const bool wave_q = qtw < nqt;
+    if (wave_q && kt <= qtw) compute(t & 1);
+    stored = false;
+    if (++kt < cur.nk) continue;
+    // ---- item done: dQ = dQ^T of this wave, lane holds query position p = 32nb + l32 ----
+    if (wave_q) {
+      float* dQg = a.dQ + base_of(cur.pair) + (size_t)qtw * 64 * rs + wd * C::DH + 4 * h;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int qin = 32 * (l32 >> 4) + 8 * ((l32 >> 2) & 3) + 4 * nb + (l32 & 3);
+#pragma unroll
+        for (int mm = 0; mm < C::MB; ++mm)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(f32x4*)(dQg + (size_t)qin * rs + 32 * mm + 8 * g) =
+                f32x4{acc[mm][nb][4 * g], acc[mm][nb][4 * g + 1], acc[mm][nb][4 * g + 2], acc[mm][nb][4 * g + 3]};
+      }
+      stored = true;
+    }
+#pragma unroll
+    for (int mm = 0; mm < C::MB; ++mm) acc[mm][0] = acc[mm][1] = zero16();
+    m = list_index(++k);
+    if (m >= nlist) break;
+    cur = item_at(m);
+    kt = 0;
+  }
+}
+
 hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s) {
   const int nqb = (a.T / 64 + 1) / 2;
-  const dim3 grid((unsigned)(a.B * a.H * nqb));
+  const int npairs = a.B * a.H;
+  if (npairs % 8 == 0) {
+    // CU count of the current device (cached per device; the query does not touch the stream)
+    static std::atomic<int> cu_cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+    int cus = dev < 64 ? cu_cache[dev].load(std::memory_order_relaxed) : 0;
+    if (cus <= 0) {
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return hipErrorInvalidDevice;
+      if (dev < 64) cu_cache[dev].store(cus, std::memory_order_relaxed);
+    }
+    // two workgroups per CU, a multiple of 8 (one share per XCD), no more than there are items
+    const int items = npairs * nqb;
+    const int per_xcd = std::max(1, std::min((2 * cus) / 8, items / 8));
+    const dim3 grid((unsigned)(8 * per_xcd));
+    if (D == 64)
+      hipLaunchKernelGGL(dqs_persistent_kernel<64>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(dqs_persistent_kernel<128>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)(npairs * nqb));
   if (D == 64)
     hipLaunchKernelGGL(dqs_kernel<64>, grid, dim3(256), 0, s, a);
   else

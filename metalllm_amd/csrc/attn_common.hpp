@@ -45,6 +45,15 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t
 __device__ __forceinline__ void dma16_v(const void* src, uint32_t m0) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
+// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima): waits until at most N of this
+// wave's vector-memory operations are outstanding. They complete in issue order, so this waits
+// for everything issued before the last N.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Waits for every vector-memory load of this wave (the untracked copies included) and every LDS
 // access, then synchronises the workgroup.
 __device__ __forceinline__ void wait_all_and_barrier() {
