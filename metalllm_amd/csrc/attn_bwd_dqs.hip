@@ -34,9 +34,11 @@ namespace mla {
 template <int D>
 struct DqsCfg {
   static constexpr int QT = 2;                       // query tiles per workgroup
-  static constexpr int KP = (D == 128) ? 144 : 80;   // K row pitch (elements): tr reads conflict-free
+  // K row pitch (elements): 320 or 192 bytes, so that the 4 rows x 64 bytes one half-wave of a
+  // ds_read_b64_tr_b16 touches (32 lanes, the LDS's 256 bytes per cycle) fall in distinct banks
+  static constexpr int KP = (D == 128) ? 160 : 96;
   static constexpr int SLOTS = KP / 8;               // 16-byte slots per padded K row = copy instructions
-  static constexpr int KPW = (SLOTS + 3) / 4;        // K copy instructions per wave (the last may repeat one)
+  static constexpr int KPW = (SLOTS + 3) / 4;        // K copy instructions per wave
   static constexpr int KBYTES = 64 * KP * 2;
   static constexpr int SBLK = 1024 + 64;             // padded 1 KB chunk row of a dS tile
   static constexpr int DSBYTES = 8 * SBLK;           // one dS tile
