@@ -42,9 +42,9 @@ struct FwdCfg {
   static constexpr int BN = kTile;       // keys per tile (64)
   static constexpr int THREADS = 256;
   static constexpr int KP = D + 8;                          // K row pitch (elements): b128 reads conflict-free
-  static constexpr int VP = (D == 128) ? D + 24 : D + 8;    // V row pitch: tr reads conflict-free
+  static constexpr int VP = D;                              // V row pitch: unpadded, XOR-swizzled
   static constexpr int KSLOTS = KP / 8;                     // 16-byte slots per K row (17 / 9)
-  static constexpr int VSLOTS = VP / 8;                     // (19 / 9)
+  static constexpr int VSLOTS = VP / 8;                     // (16 / 8)
   static constexpr int KBYTES = BN * KP * 2;                // = KSLOTS KB: one 1 KB load instruction per KB
   static constexpr int VBYTES = BN * VP * 2;
   static constexpr int STAGE = KBYTES + VBYTES;
@@ -106,10 +106,13 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     const int s = 64 * (wave + 4 * j) + lane, row = s / C::KSLOTS, c = min(s % C::KSLOTS, D / 8 - 1);
     koff[j] = (uint32_t)(row * rs * 2 + c * 16);
   }
+  // V tile, unpadded: row r, LDS chunk p holds V chunk p ^ vx(r), so that the 4 rows x 64 bytes
+  // that 32 lanes of one transposing read touch fall in distinct banks
+  auto vx = [](int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
 #pragma unroll
   for (int j = 0; j < C::VPW; ++j) {
-    const int s = 64 * (wave + 4 * j) + lane, row = s / C::VSLOTS, c = min(s % C::VSLOTS, D / 8 - 1);
-    voff[j] = (uint32_t)(row * rs * 2 + c * 16);
+    const int s = 64 * (wave + 4 * j) + lane, row = s / C::VSLOTS, p = s % C::VSLOTS;
+    voff[j] = (uint32_t)(row * rs * 2 + 16 * (p ^ vx(row)));
   }
   // The copies are untracked by the compiler (dma16): sync() waits for them before the barrier
   // that precedes any read of the stage.
@@ -132,10 +135,16 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   // Per-lane LDS operand bases (element offsets inside a stage).
   // K rows: A operand of S^T, lane = key row, 8 d at 16c + 8h.
   const int k_rd = l32 * C::KP + 8 * h;
-  // V^T via tr reads: group g = lane/16 covers d = 16(g%2) .. +15 of a 32-d tile; source lane
-  // s = lane%16 points at key row 4h + s/4 (+8 for the second read), d offset 4(s%4).
+  // V^T via tr reads: group g = lane/16 covers d = 16(g%2) .. +15 of 32-d tile dt; source lane
+  // s = lane%16 points at key row 4h + s/4 (+8 for the second read, +16c per key chunk), d offset
+  // 4(s%4). Those rows share the swizzle vx, so each d tile has one per-lane base.
   const int g16 = lane >> 4, s16 = lane & 15;
-  const int v_rd = (4 * h + (s16 >> 2)) * C::VP + 16 * (g16 & 1) + 4 * (s16 & 3);
+  int v_rd[C::DT];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) {
+    const int r = 4 * h + (s16 >> 2), ch = 4 * dt + 2 * (g16 & 1) + ((s16 & 3) >> 1);
+    v_rd[dt] = r * C::VP + 8 * (ch ^ vx(r)) + 4 * (s16 & 1);
+  }
 
   auto s_tile = [&](int stage, f32x16& S0, f32x16& S1) {
     const uint16_t* kb = (const uint16_t*)(smem + stage * C::STAGE) + k_rd;
@@ -185,7 +194,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     using F = decltype(flags);
     if (F::PV) apply_rescale();
     const uint16_t* kb = (const uint16_t*)(smem + rd * C::STAGE) + k_rd;
-    const uint16_t* vb = (const uint16_t*)(smem + rd * C::STAGE + C::KBYTES) + v_rd;
+    const uint16_t* vb = (const uint16_t*)(smem + rd * C::STAGE + C::KBYTES);
     constexpr int NSM = F::S ? 2 * C::KC : 0;  // S products
     constexpr int NPV = F::PV ? 4 * C::DT : 0;  // P.V products
     constexpr int NM = NSM + NPV;
@@ -209,8 +218,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
       const int j = index(i);
       if (kind(i)) {  // P.V product j: key chunk c, d tile dt
         const int c = j / C::DT, dt = j % C::DT;
-        const u32x2 lo = lds_tr(vb + 16 * c * C::VP + 32 * dt);
-        const u32x2 hi = lds_tr(vb + (16 * c + 8) * C::VP + 32 * dt);
+        const u32x2 lo = lds_tr(vb + v_rd[dt] + 16 * c * C::VP);
+        const u32x2 hi = lds_tr(vb + v_rd[dt] + (16 * c + 8) * C::VP);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
       return lds_read16(kb + (j & 1) * 32 * C::KP + 16 * (j >> 1));  // S product j: half j&1, d step j>>1

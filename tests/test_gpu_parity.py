@@ -64,6 +64,8 @@ CASES = [
     (1, 192, 3, 128, 1.5, 14),    # T not a multiple of 128/256, odd head count
     (1, 64, 1, 64, 1.0, 15),      # a single tile
     (3, 320, 1, 64, 1.0, 16),     # 5 tiles, B*H not a multiple of 8
+    (4, 448, 2, 128, 1.0, 17),    # 8 pairs: XCD-affine two-tile dQ ring (T < 512), 7 tiles
+    (2, 576, 4, 128, 1.0, 18),    # 8 pairs: XCD-affine four-tile dQ ring, last item 1 of 4 tiles
 ]
 
 
