@@ -19,7 +19,9 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <initializer_list>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "../../include/metalllm_attn.h"
@@ -276,17 +278,34 @@ int op_grad_dw(const Ctx& c, const uint16_t* x, const uint16_t* hi, const uint16
   return reduce_into(c, part, parts, cc, dVw, true);
 }
 
-// Zeroes n16 16-byte words (a fill kernel: no memset node when captured into a graph).
-__global__ void __launch_bounds__(256) zero_kernel(uint4* __restrict__ p, size_t n16) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
-    p[i] = uint4{0u, 0u, 0u, 0u};
+// Zeroes up to 8 buffers in one launch (a fill kernel: no memset node when captured into a
+// graph). Each segment is n16 16-byte words; grid-stride over each segment in turn.
+struct ZeroSet {
+  uint4* p[8];
+  size_t n16[8];
+  int n;
+};
+
+__global__ void __launch_bounds__(256) zero_kernel(ZeroSet z) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x, i0 = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  for (int k = 0; k < z.n; ++k)
+    for (size_t i = i0; i < z.n16[k]; i += stride) z.p[k][i] = uint4{0u, 0u, 0u, 0u};
 }
 
-int zero_bytes(const Ctx& c, void* p, size_t bytes) {  // bytes a multiple of 16
+// (pointer, bytes) pairs, bytes a multiple of 16
+int zero_buffers(const Ctx& c, std::initializer_list<std::pair<void*, size_t>> bufs) {
   if (c.query) return METALLLM_ATTN_OK;
-  const size_t n16 = bytes / 16;
-  const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 8192);
-  hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, c.stream, (uint4*)p, n16);
+  ZeroSet z{};
+  size_t largest = 0;
+  for (const auto& b : bufs) {
+    if (z.n == 8) return METALLLM_ATTN_E_LAUNCH;
+    z.p[z.n] = (uint4*)b.first;
+    z.n16[z.n] = b.second / 16;
+    largest = std::max(largest, z.n16[z.n]);
+    ++z.n;
+  }
+  const unsigned blocks = (unsigned)std::max<size_t>(1, std::min<size_t>((largest + 255) / 256, 8192));
+  hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, c.stream, z);
   return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
@@ -432,17 +451,15 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
     if (block && !c.query) TRY(residualAdd(b->hidden, b->out, b->residual, (uint32_t)e, s));  // model.h:483
     return METALLLM_ATTN_OK;
   }
-  if (block) {  // model.h:545-546
-    TRY(zero_bytes(c, b->ln_dgamma, (size_t)C * 4));
-    TRY(zero_bytes(c, b->ln_dbeta, (size_t)C * 4));
-  }
   // model.h:549-555 zeroes the accumulated gradients before the pass (the attention backward
-  // writes dQ, dK and dV in full)
-  TRY(zero_bytes(c, b->dX, e * 4));
-  TRY(zero_bytes(c, b->dQw, (size_t)C * C * 4));
-  TRY(zero_bytes(c, b->dKw, (size_t)C * C * 2));
-  TRY(zero_bytes(c, b->dVw, (size_t)C * C * 2));
-  TRY(zero_bytes(c, b->dProjw, (size_t)C * C * 2));
+  // writes dQ, dK and dV in full), and for the block model.h:545-546 the layernorm's; one launch
+  const std::pair<void*, size_t> grads[] = {{b->dX, e * 4}, {b->dQw, (size_t)C * C * 4}, {b->dKw, (size_t)C * C * 2},
+                                            {b->dVw, (size_t)C * C * 2}, {b->dProjw, (size_t)C * C * 2}};
+  if (block)
+    TRY(zero_buffers(c, {grads[0], grads[1], grads[2], grads[3], grads[4], {b->ln_dgamma, (size_t)C * 4},
+                         {b->ln_dbeta, (size_t)C * 4}}));
+  else
+    TRY(zero_buffers(c, {grads[0], grads[1], grads[2], grads[3], grads[4]}));
   TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial));
   TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
   if (!c.query) {
