@@ -275,8 +275,11 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
     auto ds_pair = [&](const f32x16& x, f32x16& y, int t, int u, float d0_, float d1_) {
       const int r = 2 * u;
       round_pair(y, r);
-      const float d0 = (x[r] * (y[r] - d0_)) * scale;
-      const float d1 = (x[r + 1] * (y[r + 1] - d1_)) * scale;
+      // D = 64: scale = 1/8 is a power of two, so bf16(v * scale) = bf16(v) / 8 exactly (above the
+      // subnormal range); dS is carried times 8 and dK, and dQ from the stored dS, are scaled once
+      // when they are stored
+      const float d0 = D == 64 ? x[r] * (y[r] - d0_) : (x[r] * (y[r] - d0_)) * scale;
+      const float d1 = D == 64 ? x[r + 1] * (y[r + 1] - d1_) : (x[r + 1] * (y[r + 1] - d1_)) * scale;
       uint32_t pk = pack_bf16(d0, d1);
       pin(pk);
       dS[8 * t + u] = pk;
@@ -377,6 +380,9 @@ __global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * dt + 8 * g + 4 * h;
+      if (D == 64) {  // dK was carried times 8 (see ds_pair); the division is exact
+        for (int u = 2 * g; u < 2 * g + 2; ++u) dKp[dt][u] = pack_bf16(bf_lo(dKp[dt][u]) * 0.125f, bf_hi(dKp[dt][u]) * 0.125f);
+      }
       *(u32x2*)(dKg + d0) = u32x2{dKp[dt][2 * g], dKp[dt][2 * g + 1]};
       *(u32x2*)(dVg + d0) = u32x2{dVp[dt][2 * g], dVp[dt][2 * g + 1]};
     }

@@ -13,7 +13,8 @@
 // 1 KB chunk rows s = 0..3, each 64 lanes x 16 bytes: lane l = key32 + 32h carries the 8 values
 // of key 32hw + key32 at query positions p = 32h + 8s + e (e = 0..7), and position p is query
 // q(p) = 32t + 8j + 4h + i of the tile with p % 32 = 16t + 4j + i. That is the order the dK/dV
-// kernel holds dS in its accumulators, so it stores with four full 16-byte writes per lane.
+// kernel holds dS in its accumulators, so it stores with four full 16-byte writes per lane. At
+// D = 64 the tiles hold 8 dS (the power-of-two scale 1/8 is applied to dQ when it is stored).
 //
 // Work split: an item is QT query tiles (64 rows each) of one (b, h); wave w of the workgroup
 // computes dQ^T of query tile qt0 + w/2 for the d half w%2, over key tiles 0 .. qt0 + QT - 1.
@@ -101,6 +102,9 @@ template <int D, int QT, int NSTAGE>
 __global__ void __launch_bounds__(128 * QT, (NSTAGE * (128 * D + 8192 * QT) <= 80 * 1024 ? 2 : 1))
 dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
   using C = DqsCfg<D, QT, NSTAGE>;
+  // the stored dS tiles of D = 64 hold 8 dS (the dK/dV kernel folds the power-of-two scale 1/8
+  // into the stores of dK and dQ): dQ = (sum of 8 dS . K) / 8, exact
+  constexpr float kDsUnit = D == 64 ? 0.125f : 1.0f;
   static_assert(C::THREADS == 128 * QT && C::WG_PER_CU == (NSTAGE * C::STAGE <= 80 * 1024 ? 2 : 1), "launch bounds");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::NSTAGE * C::STAGE];
 
@@ -266,7 +270,7 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             *(f32x4*)(dQg + (size_t)qin * rs + 32 * mm + 8 * g) =
-                f32x4{acc[mm][nb][4 * g], acc[mm][nb][4 * g + 1], acc[mm][nb][4 * g + 2], acc[mm][nb][4 * g + 3]};
+                f32x4{acc[mm][nb][4 * g], acc[mm][nb][4 * g + 1], acc[mm][nb][4 * g + 2], acc[mm][nb][4 * g + 3]} * kDsUnit;
       }
       s1 = true;
     }
