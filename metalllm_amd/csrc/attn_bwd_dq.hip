@@ -238,8 +238,9 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
         ya[u] = pa[u] * (bf_lo(db[u]) - dq);
         yb[u] = pb[u] * (bf_hi(db[u]) - dq);
         pin(ya[u], yb[u]);
-      } else {  // dS = bf16(p * (dP - D) * scale)
-        uint32_t pk = pack_bf16(ya[u] * scale, yb[u] * scale);
+      } else {  // dS = bf16(p * (dP - D) * scale); at D = 64 (scale 1/8, a power of two) dS is
+                // carried times 8 and dQ divided once when it is stored: exact above the subnormals
+        uint32_t pk = D == 64 ? pack_bf16(ya[u], yb[u]) : pack_bf16(ya[u] * scale, yb[u] * scale);
         pin(pk);
         dS[u] = pk;
       }
@@ -310,7 +311,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         *(f32x4*)(buf + l32 * C::DQP + 32 * dt + 8 * g + 4 * h) =
-            f32x4{dQa[dt][4 * g], dQa[dt][4 * g + 1], dQa[dt][4 * g + 2], dQa[dt][4 * g + 3]};
+            f32x4{dQa[dt][4 * g], dQa[dt][4 * g + 1], dQa[dt][4 * g + 2], dQa[dt][4 * g + 3]} * (D == 64 ? 0.125f : 1.0f);
   }
   __syncthreads();
   if (!wave_active) return;
