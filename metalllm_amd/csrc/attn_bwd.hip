@@ -11,8 +11,8 @@
 // when the caller provides a workspace (flashAttentionBackwardWorkspace), this kernel also
 // stores every dS tile it computes, bf16, and attn_bwd_dqs.hip computes dQ = dS.K from them.
 //
-// Work split: 4 waves x 32 keys per workgroup, two workgroups per CU. Wave w owns keys
-// 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core B operands
+// Work split: 4 waves x 32 keys per workgroup, two workgroups per CU (three at D = 64). Wave w
+// owns keys 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core B operands
 // and computes S and dP with lane = key (the query tile's Q and dO rows are A operands from
 // LDS), so P and dS come out of the accumulators already laid out as the B operands of
 // dV^T += dO^T.P and dK^T += Q^T.dS: no LDS round trip. dO^T and Q^T are read with
@@ -67,8 +67,10 @@ struct DiagTag {
   static constexpr bool value = V;
 };
 
+// D = 64: three workgroups per CU (168 VGPRs, a few spilled outside the product loop), 6-8%
+// faster than two; D = 128 needs its 244-249 VGPRs and runs two.
 template <int D, bool DS>
-__global__ void __launch_bounds__(256, 2) bwd_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
 
