@@ -12,10 +12,10 @@
 // stores every dS tile it computes, bf16, and attn_bwd_dqs.hip computes dQ = dS.K from them.
 //
 // Work split: 4 waves x 32 keys per workgroup, two workgroups per CU (three at D = 64). Wave w
-// owns keys 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core B operands
-// and computes S and dP with lane = key (the query tile's Q and dO rows are A operands from
-// LDS), so P and dS come out of the accumulators already laid out as the B operands of
-// dV^T += dO^T.P and dK^T += Q^T.dS: no LDS round trip. dO^T and Q^T are read with
+// owns keys 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core
+// B operands and computes S and dP with lane = key (the query tile's Q and dO rows are A
+// operands from LDS), so P and dS come out of the accumulators already laid out as the B
+// operands of dV^T += dO^T.P and dK^T += Q^T.dS: no LDS round trip. dO^T and Q^T are read with
 // ds_read_b64_tr_b16 from the row-major tiles, four queries per read, in the order
 // {8g + 4h + i} that lane half h holds. Between query tiles dK and dV are bf16 values (the
 // reference stores them as bf16 after every query tile), carried packed two per register and
