@@ -38,7 +38,9 @@ struct BwdCfg {
   static constexpr int BN = kBwdBlockN;  // keys per workgroup (128)
   static constexpr int BM = kTile;       // query rows per tile (the reference's query tile)
   static constexpr int THREADS = 256;
-  static constexpr int P = (D == 128) ? D + 24 : D + 8;  // Q/dO row pitch: b128 row and tr reads conflict-free
+  // Q/dO row pitch: the 16-byte row reads are conflict-free; the transposing reads take 2-way
+  // conflicts (no pitch clears both)
+  static constexpr int P = (D == 128) ? D + 24 : D + 8;
   static constexpr int TBYTES = BM * P * 2;              // one padded tile
   static constexpr int SLOTS = P / 8;                    // 16-byte slots of a padded row
   static constexpr int LPW = (SLOTS + 3) / 4;            // row-copy instructions per wave per tile (max)
