@@ -123,7 +123,8 @@ def computeD(dO, O, D, stream=None, params: AttentionParams | None = None):
 
 
 def flashAttentionBackward(dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None):
-    """attention.metal:198-299. dQ = grad (fp32); dK, dV = grads (bf16); all three written in full."""
+    """attention.metal:198-299. dQ += grad (fp32, accumulated into as the reference's atomics do: zero it
+    first for the plain gradient); dK, dV = grads (bf16), written in full."""
     p = params or _shape(q)
     _check(_lib().flashAttentionBackward(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ), _ptr(dK),
                                          _ptr(dV), ctypes.byref(p), _stream(stream)), "flashAttentionBackward")
@@ -146,7 +147,8 @@ def _ws(workspace):
 def flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, workspace, stream=None,
                                     params: AttentionParams | None = None):
     """flashAttentionBackward with a device workspace (a tensor of at least workspace_bytes bytes)
-    holding the stored dS tiles; dK, dV identical, dQ equal up to fp32 summation order."""
+    holding the stored dS tiles; dK, dV identical. dQ is written in full (= the gradient), equal to
+    what flashAttentionBackward adds into a zeroed dQ up to fp32 summation order."""
     p = params or _shape(q)
     wp, wn = _ws(workspace)
     _check(_lib().flashAttentionBackwardWorkspace(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
@@ -178,10 +180,10 @@ def attention_forward(q, k, v, stream=None):
 
 def attention_backward(dO, q, k, v, out, lse, stream=None):
     """The reference's backward sequence (model.h:639-665 dispatches): computeD,
-    flashAttentionBackward. Returns (dQ fp32, dK, dV, D)."""
+    flashAttentionBackward into a zeroed dQ (model.h:549). Returns (dQ fp32, dK, dV, D)."""
     import torch
     B, T, H, D = q.shape
-    dQ = torch.empty((B, T, H, D), dtype=torch.float32, device=q.device)
+    dQ = torch.zeros((B, T, H, D), dtype=torch.float32, device=q.device)
     dK = torch.empty_like(q)
     dV = torch.empty_like(q)
     Dv = torch.empty((B, H, T), dtype=torch.float32, device=q.device)

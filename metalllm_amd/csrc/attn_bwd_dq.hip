@@ -6,11 +6,12 @@
 //   dS = bf16(p * (dP - D[q]) * scale)                               (:284)
 //   dQ[q] += dS.K    (fp32 atomic add into the caller-zeroed dQ, :288,292-296)
 // The reference computes dS inside the key-tile owner and adds one dQ part per (key tile,
-// query tile) with fp32 atomics. Here a query-owner workgroup recomputes S, dP and dS for its
-// 128 query rows over all keys, keeps dQ in matrix-core accumulators, and writes its rows of dQ
-// once (the sum the reference's atomics build in the zeroed buffer): the device executes about
-// 0.33e12 fp32 atomic adds per second, so the owner-side form (one atomic per element per key
-// tile) would cost more than the whole kernel at long sequences. The dQ product sums each query's keys in fp32 across key tiles (the
+// query tile) with fp32 atomics into dQ. Here a query-owner workgroup recomputes S, dP and dS for
+// its 128 query rows over all keys, keeps dQ in matrix-core accumulators, and adds its sum to its
+// rows of dQ with one read-add-write per element (the only writer of those rows, so no atomics:
+// the device executes about 0.33e12 fp32 atomic adds per second, and the owner-side form, one
+// atomic per element per key tile, would cost more than the whole kernel at long sequences). dQ
+// keeps the reference's contract: the result is added to what the caller's buffer holds. The dQ product sums each query's keys in fp32 across key tiles (the
 // reference rounds each 64-key part to bf16 first, :288; the difference is far inside the
 // gradient tolerance).
 //
@@ -303,7 +304,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
     __syncthreads();
   }
 
-  // ---- dQ: transpose through LDS ([q][d] fp32), then row-contiguous stores ----
+  // ---- dQ += result: transpose through LDS ([q][d] fp32), then row-contiguous read-add-writes ----
   float* buf = (float*)smem + wave * 32 * C::DQP;
   if (wave_active) {
 #pragma unroll
@@ -319,7 +320,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
 #pragma unroll 4
   for (int r = 0; r < 32; ++r)
 #pragma unroll
-    for (int c = 0; c < D / 64; ++c) dQg[(size_t)r * rs + 64 * c + lane] = buf[r * C::DQP + 64 * c + lane];
+    for (int c = 0; c < D / 64; ++c) dQg[(size_t)r * rs + 64 * c + lane] += buf[r * C::DQP + 64 * c + lane];
 }
 
 hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s) {

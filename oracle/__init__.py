@@ -37,7 +37,8 @@ class AttentionParams(ctypes.Structure):
 
 class OracleOpts(ctypes.Structure):
     _fields_ = [("threads", ctypes.c_int), ("b_begin", ctypes.c_int), ("b_end", ctypes.c_int),
-                ("gemm_model", ctypes.c_int), ("bwd_mode", ctypes.c_int), ("d_round", ctypes.c_int)]
+                ("gemm_model", ctypes.c_int), ("bwd_mode", ctypes.c_int), ("d_round", ctypes.c_int),
+                ("fwd_lazy", ctypes.c_float)]
 
 
 def build(force: bool = False) -> str:
@@ -66,8 +67,10 @@ def params(B: int, T: int, H: int, D: int) -> AttentionParams:
 
 
 def opts(threads: int = 0, b_begin: int = 0, b_end: int = 0, gemm_model: int = GEMM_MFMA,
-         bwd_mode: int = BWD_REFERENCE, d_round: int = 1) -> OracleOpts:
-    return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round)
+         bwd_mode: int = BWD_REFERENCE, d_round: int = 1, fwd_lazy: float = 0.0) -> OracleOpts:
+    """fwd_lazy > 0 is a diagnosis mode (the GPU forward's lazy softmax reference point); 0 is the
+    reference's exact running max."""
+    return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round, fwd_lazy)
 
 
 def _check(rc: int, what: str):
@@ -85,6 +88,7 @@ class Oracle:
         pp = ctypes.POINTER(AttentionParams)
         op = ctypes.POINTER(OracleOpts)
         L.oracle_forward.argtypes = [u16p, u16p, u16p, u16p, f32p, pp, op]
+        L.oracle_forward_ex.argtypes = [u16p, u16p, u16p, u16p, f32p, f32p, pp, op]
         L.oracle_compute_d.argtypes = [u16p, u16p, f32p, pp, op]
         L.oracle_backward.argtypes = [u16p, f32p, f32p, u16p, u16p, u16p, f32p, u16p, u16p, pp, op]
         L.oracle_fill_normal_bf16.argtypes = [u16p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float]
@@ -100,6 +104,16 @@ class Oracle:
         _check(self.lib.oracle_forward(q, k, v, out, lse, ctypes.byref(params(B, T, H, D)), ctypes.byref(o or opts())),
                "forward")
         return out, lse
+
+    def forward_f32(self, q, k, v, o: OracleOpts | None = None):
+        """forward() plus O*(1/l) in fp32 before its final bf16 rounding ([B, T, H, D])."""
+        B, T, H, D = q.shape
+        out = np.zeros_like(q)
+        lse = np.zeros((B, H, T), dtype=np.float32)
+        of = np.zeros((B, T, H, D), dtype=np.float32)
+        _check(self.lib.oracle_forward_ex(q, k, v, out, lse, of, ctypes.byref(params(B, T, H, D)),
+                                          ctypes.byref(o or opts())), "forward")
+        return out, lse, of
 
     def compute_d(self, dO, O, o: OracleOpts | None = None):
         B, T, H, D = dO.shape
@@ -151,6 +165,10 @@ def normal_bf16(shape, seed: int, tensor_id: int, scale: float = 1.0) -> np.ndar
 
 def forward(q, k, v, o: OracleOpts | None = None):
     return default().forward(q, k, v, o)
+
+
+def forward_f32(q, k, v, o: OracleOpts | None = None):
+    return default().forward_f32(q, k, v, o)
 
 
 def compute_d(dO, O, o: OracleOpts | None = None):

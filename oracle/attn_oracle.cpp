@@ -21,7 +21,7 @@
 // Rounding points follow the reference (bf(x) = round fp32 -> bf16 nearest-even):
 //   S = bf(Q.K^T) [:113, bf16 LDS tile], s = bf(S*scale + mask) [:115-121],
 //   P = bf(e) with l accumulating unrounded e [:136-149], out = bf(O*(1/l)), lse = m + log(l) [:157-161],
-//   D = bf(sum_d bf(dO*O)) [:186-193],
+//   D = bf(simd_sum over lanes l of sum_{c = l mod 32} bf(dO*O)) [:186-193],
 //   dP = bf(dO.V^T), S = bf(Q.K^T) [:274-275], p = exp(S*scale - lse), diagonal mask -> 0,
 //   P = bf(p), dS = bf(p*(dP - D)*scale) [:277-286], dQpart = bf(dS.K) then fp32 add into dQ [:288,294],
 //   dK = bf(dK + dS^T.Q), dV = bf(dV + P^T.dO) once per 64-row query tile [:289-290].
@@ -75,6 +75,10 @@ typedef struct {
   int bwd_mode;     // BWD_REFERENCE: bf16 dK/dV per query tile and bf16 dQ parts (as the reference);
                     // BWD_FP32: fp32 accumulation, one rounding of dK/dV at the end
   int d_round;      // 1: D rounded to bf16 (the reference stores bf16 D); 0: fp32 D
+  float fwd_lazy;   // 0: the reference's running max (moves to every larger tile max, :127-134).
+                    // t > 0: a diagnosis mode that moves the softmax reference point only when the
+                    // tile max exceeds it by more than t in log2 units, as the GPU forward does
+                    // (t = 8); P = bf16(exp(s - m)) is then rounded relative to that point
 } OracleOpts;
 
 }  // extern "C"
@@ -314,7 +318,7 @@ Slice slice_of(const AttentionParams& p, const OracleOpts* o) {
 
 // flashAttentionForward for one (b,h): attention.metal:74-163.
 void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* lse,
-                  const AttentionParams& p, uint32_t b, uint32_t h, int model) {
+                  float* out_f32, const AttentionParams& p, uint32_t b, uint32_t h, int model, float lazy) {
   const int T = (int)p.M, D = (int)p.D, ntiles = T / TILE;
   Mat Q, K, V, P, Vt;
   gather_head(q, p, b, h, Q);
@@ -343,6 +347,7 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
         float mx = -INFINITY;
         for (int c = 0; c < TILE; ++c) mx = std::max(mx, sr[c]);
         mx = std::max(mx, m[r]);
+        if (lazy > 0.0f && m[r] != -INFINITY && (mx - m[r]) * 1.4426950408889634f <= lazy) mx = m[r];
         const float a = std::exp(m[r] - mx);
         float sum = 0.0f;
         for (int c = 0; c < TILE; ++c) {
@@ -367,6 +372,10 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
       lse[((size_t)b * p.NH + h) * p.M + t] = m[r] + std::log(l[r]);
       uint16_t* orow = out + ((size_t)b * p.M + t) * p.N + (size_t)h * D;
       for (int d = 0; d < D; ++d) orow[d] = f2bf(O[(size_t)r * D + d] * inv);
+      if (out_f32) {  // the value the final bf16 rounding sees (diagnosis of output rounding flips)
+        float* frow = out_f32 + ((size_t)b * p.M + t) * p.N + (size_t)h * D;
+        for (int d = 0; d < D; ++d) frow[d] = O[(size_t)r * D + d] * inv;
+      }
     }
   }
 }
@@ -463,21 +472,30 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
 
 extern "C" {
 
-int oracle_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* lse,
-                   const AttentionParams* p, const OracleOpts* o) {
+// out_f32 (optional, may be NULL): fp32 [B,T,H,D], O*(1/l) before its bf16 rounding.
+int oracle_forward_ex(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* lse,
+                      float* out_f32, const AttentionParams* p, const OracleOpts* o) {
   if (!valid(p) || !q || !k || !v || !out || !lse) return -1;
   const Slice s = slice_of(*p, o);
   const int model = o ? o->gemm_model : GEMM_MFMA;
+  const float lazy = o ? o->fwd_lazy : 0.0f;
   const int nwork = (int)((s.b1 - s.b0) * p->NH);
   parallel_for(nwork, o ? o->threads : 0, [&](int i) {
-    forward_head(q, k, v, out, lse, *p, s.b0 + (uint32_t)i / p->NH, (uint32_t)i % p->NH, model);
+    forward_head(q, k, v, out, lse, out_f32, *p, s.b0 + (uint32_t)i / p->NH, (uint32_t)i % p->NH, model, lazy);
   });
   return 0;
 }
 
-// computeD: attention.metal:179-194. Each product is rounded to bf16 (MSL bfloat*bfloat), and
-// summed in fp32: 8 consecutive columns sequentially, then the D/8 partial sums pairwise
-// (p0+p1, p2+p3, ... then again), the order of a lane-segment sum followed by a xor-butterfly.
+int oracle_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* lse,
+                   const AttentionParams* p, const OracleOpts* o) {
+  return oracle_forward_ex(q, k, v, out, lse, nullptr, p, o);
+}
+
+// computeD: attention.metal:179-194. One 32-lane simdgroup per row (:186): lane l sums the
+// columns l, l+32, l+64, l+96 (< D) of bf16(dO*O) in that order in fp32, starting from 0.0f
+// (:188-191; MSL bfloat*bfloat is rounded to bfloat); simd_sum then adds the 32 lane sums (:192).
+// Apple does not publish simd_sum's order; it is modelled as the xor butterfly (partners at
+// distance 16, 8, 4, 2, 1). The result is stored as bf16 (:193).
 int oracle_compute_d(const uint16_t* dO, const uint16_t* O, float* Dout, const AttentionParams* p,
                      const OracleOpts* o) {
   if (!valid(p) || !dO || !O || !Dout) return -1;
@@ -488,16 +506,18 @@ int oracle_compute_d(const uint16_t* dO, const uint16_t* O, float* Dout, const A
     const uint32_t b = s.b0 + (uint32_t)i / p->M, t = (uint32_t)i % p->M;
     for (uint32_t h = 0; h < p->NH; ++h) {
       const size_t base = ((size_t)b * p->M + t) * p->N + (size_t)h * p->D;
-      float part[16];
-      const int nch = (int)p->D / 8;
-      for (int c = 0; c < nch; ++c) {
+      float lane_sum[32];
+      for (int l = 0; l < 32; ++l) {
         float acc = 0.0f;
-        for (int j = 0; j < 8; ++j) acc += bf(bf2f(dO[base + c * 8 + j]) * bf2f(O[base + c * 8 + j]));
-        part[c] = acc;
+        for (int c = l; c < (int)p->D; c += 32) acc += bf(bf2f(dO[base + c]) * bf2f(O[base + c]));
+        lane_sum[l] = acc;
       }
-      for (int w = 1; w < nch; w *= 2)
-        for (int c = 0; c < nch; c += 2 * w) part[c] = part[c] + part[c + w];
-      Dout[((size_t)b * p->NH + h) * p->M + t] = dround ? bf(part[0]) : part[0];
+      for (int w = 16; w >= 1; w /= 2) {
+        float nxt[32];
+        for (int l = 0; l < 32; ++l) nxt[l] = lane_sum[l] + lane_sum[l ^ w];
+        std::memcpy(lane_sum, nxt, sizeof(nxt));
+      }
+      Dout[((size_t)b * p->NH + h) * p->M + t] = dround ? bf(lane_sum[0]) : lane_sum[0];
     }
   });
   return 0;

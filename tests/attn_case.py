@@ -46,11 +46,13 @@ def gpu_forward(q, k, v, dev):
 
 def gpu_backward(g, Dv, lse, q, k, v, dev, workspace=False):
     """flashAttentionBackward (or, with workspace, flashAttentionBackwardWorkspace) alone on given
-    D / lse. The outputs start filled with NaN: the backward writes them in full."""
+    D / lse. dK and dV start filled with NaN (both entry points write them in full); dQ starts at
+    zero for flashAttentionBackward, which adds into it as the reference does, and at NaN for the
+    workspace variant, which writes it in full."""
     import torch
     import metalllm_amd as M
     tq, tk, tv, tg = (to_gpu(x, dev) for x in (q, k, v, g))
-    dQ = torch.full(q.shape, float("nan"), dtype=torch.float32, device=dev)
+    dQ = torch.full(q.shape, float("nan") if workspace else 0.0, dtype=torch.float32, device=dev)
     dK = torch.full_like(tq, float("nan"))
     dV = torch.full_like(tq, float("nan"))
     if workspace:
@@ -88,6 +90,21 @@ def out_error(out_gpu, out_ref):
     d = np.abs(a - b)
     bar = np.maximum(np.float32(1e-2), bf16_ulp(b))
     return float(d.max()), int((d > bar).sum()), int((d > 1e-2).sum())
+
+
+def out_exceptions(out_gpu, out_ref_f32, bar=1e-2):
+    """Elements of O beyond the north_star's 1e-2 max-abs bar, each classified. An element whose
+    magnitude is at least 2 has a bf16 spacing of 1/64 > 1e-2, so two correct roundings of values
+    a hair apart can differ by one spacing: such an element is an output rounding flip when the
+    GPU's bf16 value is within one spacing of the oracle's unrounded fp32 value (O*(1/l) before its
+    final rounding, attention.metal:161). Returns (flips, unexplained) as lists of flat indices."""
+    a = f32(out_gpu).ravel()
+    x = np.asarray(out_ref_f32, dtype=np.float32).ravel()
+    ref = f32(O.f32_to_bf16(x))
+    over = np.nonzero(np.abs(a - ref) > bar)[0]
+    ulp = bf16_ulp(x[over])
+    is_flip = (np.abs(x[over]) >= 2.0) & (np.abs(a[over] - x[over]) <= ulp)
+    return over[is_flip].tolist(), over[~is_flip].tolist()
 
 
 def rel_to_max(x, ref):

@@ -1,12 +1,14 @@
 """GPU parity: the HIP kernels through the C ABI against the CPU oracle on identical seeded inputs.
 
-Bars: LSE within 1e-3; O within 1e-2 max-abs, except elements whose
-bf16 spacing exceeds 1e-2 (|O| >= 2), where the bar is one bf16 ulp of the oracle's value;
-dQ/dK/dV within 2e-2 max-abs relative to max |grad|; computeD bit-exact (same inputs, same
-summation order); causal-mask and index logic exact (row 0 of O equals row 0 of V bit for bit).
-Both backward entry points are checked: flashAttentionBackward and flashAttentionBackwardWorkspace
-(the stored-dS path); their dK/dV must also be identical to each other, their dQ equal within
-1e-5 of max |dQ| (fp32 summation order).
+Bars: LSE within 1e-3; O within 1e-2 max-abs, where every element
+beyond it is listed and must be an output rounding flip (|O| >= 2, whose bf16 spacing 1/64
+exceeds the bar, and within one spacing of the oracle's unrounded value); dQ/dK/dV within 2e-2
+max-abs relative to max |grad|; computeD bit-exact (the reference's lane-strided sums and the
+oracle's butterfly model of simd_sum); causal-mask and index logic exact (row 0 of O equals row 0
+of V bit for bit; with V one-hot every future weight is exactly zero). Both backward entry points
+are checked: flashAttentionBackward (which adds into dQ, as the reference's atomics do) and
+flashAttentionBackwardWorkspace (the stored-dS path, which writes dQ); their dK/dV must also be
+identical to each other, their dQ equal within 1e-5 of max |dQ| (fp32 summation order).
 """
 import ctypes
 import os
@@ -15,8 +17,9 @@ import numpy as np
 import pytest
 
 import oracle as O
-from tests.attn_case import (f32, gpu_backward, gpu_compute_d, gpu_forward, make_inputs, out_error, rel_to_max,
-                             to_gpu, to_np)
+from tests.attn_case import (f32, gpu_backward, gpu_compute_d, gpu_forward, make_inputs, out_error, out_exceptions,
+                             rel_to_max, to_gpu, to_np)
+from tests.lse_flips import diagnose_row, rows_beyond
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -28,14 +31,16 @@ def check_case(gpu, B, T, H, D, s, seed, b_end=0, threads=0):
     q, k, v, g = make_inputs(B, T, H, D, seed, s)
     nb = b_end or B
     sl = lambda x: np.ascontiguousarray(x[:nb])
-    r_out, r_lse = O.forward(sl(q), sl(k), sl(v), O.opts(threads=threads))
+    r_out, r_lse, r_of = O.forward_f32(sl(q), sl(k), sl(v), O.opts(threads=threads))
     ref = {"out": r_out, "lse": r_lse}
     out, lse = gpu_forward(q, k, v, gpu)
     lse_err = float(np.abs(lse[:nb] - ref["lse"]).max())
-    o_max, o_bad, o_over = out_error(out[:nb], ref["out"])
-    print(f"  fwd: lse max err {lse_err:.3g}, O max err {o_max:.3g}, O beyond bar {o_bad}, O > 1e-2 {o_over}")
+    o_max, _, o_over = out_error(out[:nb], ref["out"])
+    flips, unexplained = out_exceptions(out[:nb], r_of)
+    print(f"  fwd: lse max err {lse_err:.3g}, O max err {o_max:.3g}, O > 1e-2: {o_over} "
+          f"(output rounding flips {len(flips)}, unexplained {len(unexplained)})")
     assert np.isfinite(lse).all() and lse_err <= 1e-3
-    assert o_bad == 0
+    assert not unexplained, unexplained[:10]
     # computeD on the GPU's own O; the oracle on the same O must agree bit for bit
     Dfull = gpu_compute_d(g, out, gpu)
     Dr = O.compute_d(sl(g), sl(out))
@@ -159,10 +164,12 @@ def test_mfma_model_on_random_tiles(gpu):
     assert bad == 0, f"{bad} of {n * 1024} results differ from the model"
 
 
-def test_backward_writes_gradients_in_full(gpu):
-    """ABI contract: dQ, dK and dV are written in full (stale contents ignored: the result equals
-    the reference's accumulation into zeroed buffers), by both entry points, and a workspace's
-    stale contents do not matter either."""
+def test_backward_dq_contract(gpu):
+    """ABI contract. flashAttentionBackward adds the gradient into dQ (the reference's fp32 atomics
+    into a caller-zeroed buffer, attention.metal:292-296, model.h:549): with dQ prefilled, the
+    result is prefill + gradient, each element one fp32 add of the zero-start result. It writes dK
+    and dV in full (stale contents ignored). flashAttentionBackwardWorkspace writes all three in
+    full, whatever the stale contents of its outputs or of the workspace."""
     import torch
     import metalllm_amd as M
     for T in (256, 192):
@@ -171,22 +178,83 @@ def test_backward_writes_gradients_in_full(gpu):
         out, lse = M.attention_forward(tq, tk, tv)
         Dv = torch.empty((1, 2, T), dtype=torch.float32, device=gpu)
         M.computeD(tg, out, Dv)
+        dQ0 = torch.zeros((1, T, 2, 64), dtype=torch.float32, device=gpu)
+        dK0, dV0 = torch.full_like(tq, float("nan")), torch.full_like(tq, float("nan"))
+        M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ0, dK0, dV0)
+        assert torch.isfinite(dQ0).all() and torch.isfinite(dK0.float()).all() and torch.isfinite(dV0.float()).all()
+        gen = torch.Generator(device=gpu)
+        gen.manual_seed(T)
+        prefill = torch.randn((1, T, 2, 64), generator=gen, device=gpu) * 3.0
+        dQ = prefill.clone()
+        dK, dV = torch.full_like(tq, 7.0), torch.full_like(tq, -7.0)
+        M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
+        assert torch.equal(dQ, prefill + dQ0)
+        assert torch.equal(dK, dK0) and torch.equal(dV, dV0)
         ws = torch.full((M.workspace_bytes(1, T, 2, 64),), 0x7F, dtype=torch.uint8, device=gpu)
-        res = []
-        for fill in (0.0, 7.0, float("nan")):
-            for use_ws in (False, True):
-                dQ = torch.full((1, T, 2, 64), fill, dtype=torch.float32, device=gpu)
-                dK = torch.full_like(tq, fill)
-                dV = torch.full_like(tq, -fill)
-                if use_ws:
-                    M.flashAttentionBackwardWorkspace(tg, Dv, lse, tq, tk, tv, dQ, dK, dV, ws)
-                else:
-                    M.flashAttentionBackward(tg, Dv, lse, tq, tk, tv, dQ, dK, dV)
-                res.append((use_ws, dQ, dK, dV))
-        for use_ws, dQ, dK, dV in res:
-            ref = res[0] if not use_ws else res[1]
-            assert torch.isfinite(dQ).all() and torch.equal(dQ, ref[1])
-            assert torch.equal(dK, res[0][2]) and torch.equal(dV, res[0][3])
+        for fill in (7.0, float("nan")):
+            wQ = torch.full_like(dQ0, fill)
+            wK, wV = torch.full_like(tq, fill), torch.full_like(tq, -fill)
+            M.flashAttentionBackwardWorkspace(tg, Dv, lse, tq, tk, tv, wQ, wK, wV, ws)
+            assert torch.isfinite(wQ).all()
+            assert (wQ - dQ0).abs().max().item() <= 1e-5 * dQ0.abs().max().item()
+            assert torch.equal(wK, dK0) and torch.equal(wV, dV0)
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 64, 1, 64), (2, 128, 3, 128), (1, 64, 2, 128), (2, 192, 4, 128),
+                                     (4, 256, 2, 64)])
+def test_causal_mask_with_one_hot_v(gpu, B, T, H, D):
+    """The causal mask pinned on the GPU (attention.metal:117-120): with V[t] = e_(t mod D), O[i]
+    carries the softmax weight of key j in column j mod D, so for rows i < D every column d > i
+    (keys that exist only in the future) must be exactly 0, every column d <= i positive, and each
+    row must sum to 1 within bf16 rounding. T = 64 and 192 leave the last 128-row block of the
+    forward half empty; T = 256 at D = 64 checks rows 0-63 over two key tiles per block."""
+    print(f"case B={B} T={T} H={H} D={D}", flush=True)
+    q, k, _, _ = make_inputs(B, T, H, D, 51)
+    v = np.zeros((B, T, H, D), np.uint16)
+    t = np.arange(T)
+    v[:, t, :, t % D] = 0x3F80  # bf16 1.0
+    out, lse = gpu_forward(q, k, v, gpu)
+    A = f32(out)  # [B, T, H, D]
+    n = min(T, D)
+    for b in range(B):
+        for h in range(H):
+            P = A[b, :n, h, :n]
+            assert (P[np.triu_indices(n, 1)] == 0).all()
+            assert (P[np.tril_indices(n)] > 0).all()
+    assert np.abs(A.sum(-1) - 1).max() < 1e-2
+    r_out, r_lse = O.forward(q, k, v)
+    assert np.abs(lse - r_lse).max() <= 1e-3
+    assert np.abs(A - f32(r_out)).max() <= 1e-2
+
+
+def test_config2_against_plain_fp32_order(gpu):
+    """Config 2 slice (seed 22, batches 0-1, all 12 heads, Q/K x1.5) against the oracle with the
+    plain sequential fp32 order of the reference's matmul2d semantics (GEMM_SEQ), not the
+    matrix-core order the GPU executes. Every LSE row beyond 1e-3 must be a diagnosed bf16
+    rounding flip of a score (the exact product within fp32 summation error of a bf16 midpoint;
+    the LSE difference equal to what that one-ulp score move produces, at most one step times the
+    flipped key's weight); every O element beyond 1e-2 must lie in such a row or be an output
+    rounding flip."""
+    B, T, H, D, s, seed, nb = 32, 1024, 12, 64, 1.5, 22, 2
+    q, k, v, _ = make_inputs(B, T, H, D, seed, s)
+    sl = lambda x: np.ascontiguousarray(x[:nb])
+    qs, ks = sl(q), sl(k)
+    r_out, r_lse, r_of = O.forward_f32(qs, ks, sl(v), O.opts(gemm_model=O.GEMM_SEQ))
+    out, lse = gpu_forward(q, k, v, gpu)
+    lse = np.ascontiguousarray(lse[:nb])
+    rows = rows_beyond(r_lse, lse)
+    diag = [diagnose_row(qs, ks, r_lse, lse, *r, O.GEMM_SEQ, O.GEMM_MFMA) for r in rows]
+    for d in diag:
+        print("  diagnosed LSE flip:", d)
+        assert d["flips"] and abs(d["observed"]) <= d["max_score_step"] * d["flip_weight"] + 5e-5
+    print(f"  LSE max err {np.abs(r_lse - lse).max():.3g}; rows beyond 1e-3: {len(rows)}, all diagnosed flips")
+    assert len(rows) <= 3
+    flips, unexplained = out_exceptions(out[:nb], r_of)
+    flip_rows = {(b, t, h) for b, h, t in rows}  # O is [B, T, H, D]
+    shape = out[:nb].shape
+    rest = [i for i in unexplained if tuple(int(x) for x in np.unravel_index(i, shape)[:3]) not in flip_rows]
+    print(f"  O > 1e-2: output rounding flips {len(flips)}, in LSE-flip rows {len(unexplained) - len(rest)}, other {len(rest)}")
+    assert not rest
 
 
 def test_backward_parts_equal_flash_attention_backward(gpu):
@@ -203,7 +271,7 @@ def test_backward_parts_equal_flash_attention_backward(gpu):
     for first in (0, 2):
         res = []
         for split in (False, True):
-            dQ = torch.empty((2, 512, 3, 128), dtype=torch.float32, device=gpu)
+            dQ = torch.zeros((2, 512, 3, 128), dtype=torch.float32, device=gpu)  # part 1 adds into dQ
             dK = torch.empty_like(tq)
             dV = torch.empty_like(tq)
             if split:
