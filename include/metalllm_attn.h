@@ -60,7 +60,9 @@ enum {
   METALLLM_ATTN_E_SIZE = -5,     /* a tensor exceeds 2^31 elements */
   METALLLM_ATTN_E_ALIGN = -6,    /* a tensor pointer is not 16-byte aligned */
   METALLLM_ATTN_E_LAUNCH = -7,   /* the kernel launch failed */
-  METALLLM_ATTN_E_LIBRARY = -8   /* a platform library call (rocBLAS, device allocation) failed */
+  METALLLM_ATTN_E_LIBRARY = -8,  /* a platform library call (rocBLAS, device allocation) failed */
+  METALLLM_ATTN_E_CAPTURE = -9   /* per-device scratch would have to grow while the stream is being
+                                    captured into a graph: call metalllmSublayerReserve first */
 };
 
 /* Replaces the flashAttentionForward dispatch at model.h:459-473 (attention.metal:56-164).
@@ -114,9 +116,19 @@ int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const fl
  * (model.h:549-555). Validation: M, B, NH, D >= 1, N == NH*D a multiple of 8, tensors below 2^31
  * elements, non-NULL 16-byte aligned pointers. The first call on a device creates that device's
  * rocBLAS handle; computeGradDx/Dw keep a per-device buffer for the two-term bf16 split of dQ, and
- * projBackwarddW/computeGradDw one for fp32 partial sums of the weight gradients (both grown on
- * demand and kept until the process ends), so those calls must not overlap on different streams
- * of one device. Asynchronous on `stream`. */
+ * projBackwarddW/computeGradDw one for fp32 partial sums of the weight gradients (both kept until
+ * the process ends), so those calls must not overlap on different streams of one device.
+ * Asynchronous on `stream`, except that a call which needs a larger buffer than the device holds
+ * grows it: hipDeviceSynchronize, then hipFree and hipMalloc (refused with
+ * METALLLM_ATTN_E_CAPTURE while `stream` is being captured into a graph). metalllmSublayerReserve
+ * sizes the buffers once, after which calls at that shape or smaller never allocate or
+ * synchronise. */
+
+/* Sizes the current device's sublayer scratch (dQ split, weight-gradient partials, the phase
+ * encoder's attention workspace) for shape p, synchronising the device if a buffer grows; the
+ * GEMM entry points and metalllmSublayerEncode at shapes up to p then run without allocating.
+ * No counterpart in the reference (model.h allocates every buffer once, :236-277). */
+int metalllmSublayerReserve(const AttentionParams* p);
 
 /* attention.metal:19-53, dispatched at model.h:446-457: q = X.q_w, k = X.k_w, v = X.v_w. */
 int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w, const uint16_t* k_w,
@@ -238,7 +250,8 @@ typedef struct metalllmSublayerGraph metalllmSublayerGraph;
  * dStream, then runs layernormBackward(dStream) and residualAdd(dStream, dOut -> dStream).
  * Validation: the GEMM rules and the attention rules above, every pointer the phase uses.
  * Uses the device's shared rocBLAS handle and scratch like the GEMM entry points above (plus a
- * per-device attention workspace, metalllmAttnBackwardWorkspaceSize bytes, grown on demand). */
+ * per-device attention workspace, metalllmAttnBackwardWorkspaceSize bytes, grown on demand with
+ * the same device synchronisation; metalllmSublayerReserve avoids it). */
 int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,
                            metalllm_stream_t stream);
 

@@ -22,14 +22,15 @@ LIB_PATH = os.path.join(PKG, "libmetalllm_attn.so")
 OK = 0
 ERRORS = {
     -1: "E_NULL", -2: "E_SEQLEN", -3: "E_HEADDIM", -4: "E_LAYOUT", -5: "E_SIZE", -6: "E_ALIGN", -7: "E_LAUNCH",
-    -8: "E_LIBRARY",
+    -8: "E_LIBRARY", -9: "E_CAPTURE",
 }
 EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "metalllmAttnBackwardPart",
             "metalllmAttnErrorString", "metalllmAttnWorkMap", "computeQKV", "projForward", "projBackwarddW",
             "projBackwarddX", "computeGradDx", "computeGradDw", "castFloatToBfloat", "metalllmSublayerEncode",
             "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize", "residualAdd",
             "layernormForward", "layernormBackward",
-            "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy")
+            "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy",
+            "metalllmSublayerReserve")
 
 
 class AttentionParams(ctypes.Structure):

@@ -109,6 +109,7 @@ const char* metalllmAttnErrorString(int code) {
     case METALLLM_ATTN_E_ALIGN: return "tensor pointers must be 16-byte aligned";
     case METALLLM_ATTN_E_LAUNCH: return "kernel launch failed";
     case METALLLM_ATTN_E_LIBRARY: return "platform library call (rocBLAS, device allocation) failed";
+    case METALLLM_ATTN_E_CAPTURE: return "scratch would grow during stream capture (call metalllmSublayerReserve first)";
     default: return "unknown error";
   }
 }

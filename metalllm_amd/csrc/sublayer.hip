@@ -55,10 +55,15 @@ struct DeviceState {
   size_t attn_ws_bytes = 0;
 };
 
-// Grows a per-device buffer (never shrinks; the old one is freed after the device drained).
+// Grows a per-device buffer (never shrinks). Growing synchronises the device (the old buffer may
+// still be in use by work enqueued on any stream) and allocates, so it is refused while `stream`
+// is being captured into a graph: metalllmSublayerReserve sizes the buffers ahead of time.
 template <typename T>
-int ensure(T*& buf, size_t& have, size_t need) {
+int ensure(T*& buf, size_t& have, size_t need, hipStream_t stream) {
   if (have >= need) return METALLLM_ATTN_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
+  if (cap != hipStreamCaptureStatusNone) return METALLLM_ATTN_E_CAPTURE;
   if (buf) {
     if (hipDeviceSynchronize() != hipSuccess || hipFree(buf) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
     buf = nullptr;
@@ -348,7 +353,7 @@ int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProj
   const int R = (int)(p->B * p->M), C = (int)p->N;
   Public u(stream);
   TRY(u.s.rc);
-  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, (size_t)row_chunks(R) * C * C));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, (size_t)row_chunks(R) * C * C, u.c.stream));
   return op_proj_dw(u.c, attn_out, dZ, dProjw, R, C, u.s.st->partial);
 }
 
@@ -369,7 +374,7 @@ int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint1
   const size_t e = (size_t)R * C;
   Public u(stream);
   TRY(u.s.rc);
-  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e));
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e, u.c.stream));
   TRY(split_dq(u.c, dQ, e, u.s.st->split));
   return op_grad_dx(u.c, dX, qw, kw, vw, u.s.st->split, u.s.st->split + e, dK, dV, R, C);
 }
@@ -382,8 +387,8 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
   const size_t e = (size_t)R * C;
   Public u(stream);
   TRY(u.s.rc);
-  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e));
-  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C));
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e, u.c.stream));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, u.c.stream));
   TRY(split_dq(u.c, dQ, e, u.s.st->split));
   return op_grad_dw(u.c, x, u.s.st->split, u.s.st->split + e, dK, dV, dQw, dKw, dVw, R, C, u.s.st->partial);
 }
@@ -537,12 +542,27 @@ int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const At
   TRY(u.s.rc);
   uint64_t ws = 0;
   if (phase == 1) {
-    TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C));
-    TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C));
+    TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C, u.c.stream));
+    TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, u.c.stream));
     TRY(metalllmAttnBackwardWorkspaceSize(p, &ws));
-    TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws));
+    TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws, u.c.stream));
   }
   return encode(u.c, phase, b, p, u.s.st->split, u.s.st->partial, u.s.st->attn_ws, ws);
+}
+
+int metalllmSublayerReserve(const AttentionParams* p) {
+  TRY(validate_gemm(p));
+  if (p->D != 64 && p->D != 128) return METALLLM_ATTN_E_HEADDIM;
+  if (p->M % 64) return METALLLM_ATTN_E_SEQLEN;
+  const int R = (int)(p->B * p->M), C = (int)p->N;
+  uint64_t ws = 0;
+  TRY(metalllmAttnBackwardWorkspaceSize(p, &ws));
+  Public u(nullptr);
+  TRY(u.s.rc);
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C, nullptr));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, nullptr));
+  TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws, nullptr));
+  return METALLLM_ATTN_OK;
 }
 
 int metalllmSublayerGraphCreate(int phase, const metalllmSublayerBuffers* b, const AttentionParams* p,

@@ -38,7 +38,8 @@ def _L():
         L.metalllmSublayerGraphCreate.argtypes = [ctypes.c_int, bp, pp, ctypes.POINTER(vp)]
         L.metalllmSublayerGraphLaunch.argtypes = [vp, vp]
         L.metalllmSublayerGraphDestroy.argtypes = [vp]
-        for f in (L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw,
+        L.metalllmSublayerReserve.argtypes = [pp]
+        for f in (L.metalllmSublayerReserve, L.computeQKV, L.projForward, L.projBackwarddW, L.projBackwarddX, L.computeGradDx, L.computeGradDw,
                   L.metalllmSublayerEncode, L.metalllmSublayerGraphCreate,
                   L.metalllmSublayerGraphLaunch, L.metalllmSublayerGraphDestroy):
             f.restype = ctypes.c_int
@@ -97,6 +98,12 @@ def computeGradDw(x, dQ, dK, dV, dQw, dKw, dVw, p: AttentionParams, stream=None)
     """attention.metal:343-383: dQw += x^T.dQ (fp32); dKw, dVw += x^T.dK, x^T.dV (bf16); accumulated."""
     _check(_L().computeGradDw(_ptr(x), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dQw), _ptr(dKw), _ptr(dVw),
                               ctypes.byref(p), _stream(stream)), "computeGradDw")
+
+
+def reserve(p: AttentionParams):
+    """metalllmSublayerReserve: size the current device's scratch for shape p once (synchronises
+    the device if it grows), so later GEMM and encoder calls up to that shape never allocate."""
+    _check(_L().metalllmSublayerReserve(ctypes.byref(p)), "metalllmSublayerReserve")
 
 
 def encode_phase(phase: int, bufs: SublayerBuffers, p: AttentionParams, stream=None):

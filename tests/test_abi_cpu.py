@@ -105,8 +105,19 @@ def test_workspace_size_and_validation():
 
 def test_error_strings():
     lib = M.library()
-    for code in range(-7, 1):
+    for code in range(-9, 1):
         assert lib.metalllmAttnErrorString(code)
+    assert lib.metalllmAttnErrorString(-9) != lib.metalllmAttnErrorString(-100)
+
+
+def test_sublayer_reserve_validates_before_device():
+    """metalllmSublayerReserve rejects shapes the sublayer cannot run before touching the device."""
+    lib = M.library()
+    lib.metalllmSublayerReserve.argtypes = [ctypes.POINTER(AttentionParams)]
+    assert lib.metalllmSublayerReserve(None) == -1
+    for fields, code in (((0, 768, 64, 12, 8), -2), ((2048, 767, 64, 12, 8), -4), ((2048, 1536, 128, 8, 8), -4),
+                         ((2048, 96 * 8, 96, 8, 8), -3), ((2000, 768, 64, 12, 8), -2)):
+        assert lib.metalllmSublayerReserve(ctypes.byref(AttentionParams(*fields))) == code, fields
 
 
 GEMM_ARGS = {  # entry point -> number of tensor pointers before the params pointer

@@ -14,6 +14,7 @@ import pytest
 
 import oracle as O
 from tests.attn_case import to_gpu, to_np
+from tests.sublayer_check import check_sublayer
 
 pytestmark = pytest.mark.gpu
 
@@ -86,6 +87,8 @@ def test_encoder_matches_per_call_chain(gpu, S):
         print(f"{n}: {'identical' if same else 'DIFFERENT'}")
         assert same, n
     assert np.array_equal(rb["dXb"], O.castFloatToBfloat(rb["dX"]))
+    # and the encoder's own results against the oracle, stage by stage
+    check_sublayer(b, to_np(dOut), batches=[0, 1], label="encoder")
 
 
 def test_graph_replays_match_encoder(gpu, S):
@@ -114,6 +117,8 @@ def test_graph_replays_match_encoder(gpu, S):
             for n in OUTPUTS + ("dXb",):
                 assert np.array_equal(rg[n], re[n]), (B, T, H, C, it, n)
             print(f"shape {(B, T, H, C)} replay {it}: identical to the encoder")
+            if it == 0:  # the replay's own results against the oracle
+                check_sublayer(g, to_np(d), batches=[B - 1], label=f"graph replay {(B, T, H, C)}")
         g.close()
 
 

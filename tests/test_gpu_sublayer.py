@@ -11,6 +11,7 @@ import pytest
 
 import oracle as O
 from tests.attn_case import bf16_ulp, f32, to_gpu, to_np
+from tests.sublayer_check import check_sublayer
 
 pytestmark = pytest.mark.gpu
 
@@ -109,48 +110,46 @@ def test_backward_gemms(gpu, S):
         assert bad == 0
 
 
-def test_config4_sublayer_chain(gpu, S):
-    """Config 4's sublayer (C=768, H=12, D=64, T=2048) at B=1: the model.h launch sequence on the GPU;
-    every stage checked against the oracle on the GPU's own inputs to that stage (attention by the
-    bars of the attention parity tests)."""
+def _run_chain(S, gpu, B, T, H, C, seed):
     import torch
-    B, T, H, C = 1, 2048, 12, 768
     R = B * T
-    X, (Wq, Wk, Wv, Wp) = inputs(R, C, 4)
-    rng = np.random.default_rng(5)
+    X, (Wq, Wk, Wv, Wp) = inputs(R, C, seed)
+    rng = np.random.default_rng(seed + 1)
     dOut = O.f32_to_bf16(rng.standard_normal((R, C)).astype(np.float32))
     tX = to_gpu(X.reshape(B, T, C), gpu)
     Ws = [to_gpu(w, gpu) for w in (Wq, Wk, Wv, Wp)]
     sub = S.Sublayer(tX, *Ws, H=H)
     sub.zero_grads()
-    out = sub.forward()
+    sub.forward()
     sub.backward(to_gpu(dOut.reshape(B, T, C), gpu))
     torch.cuda.synchronize()
-    n = lambda t: to_np(t).reshape(R, C) if t.dim() == 3 else to_np(t)
-    # forward stages
-    rq, rk, rv = O.computeQKV(X, Wq, Wk, Wv, threads=16)
-    for g, r in ((sub.q, rq), (sub.k, rk), (sub.v, rv)):
-        assert bf_err(n(g), r)[0] == 0
-    q4 = lambda a: np.ascontiguousarray(a.reshape(B, T, H, C // H))
-    r_o, r_lse = O.forward(q4(n(sub.q)), q4(n(sub.k)), q4(n(sub.v)), O.opts(threads=16))
-    assert float(np.abs(to_np(sub.lse) - r_lse).max()) <= 1e-3
-    assert float(np.abs(f32(n(sub.o)) - f32(r_o.reshape(R, C))).max()) <= 1e-2
-    assert bf_err(n(out), O.projForward(n(sub.o), Wp, threads=16))[0] == 0
-    # backward stages
-    rWp = O.projBackwarddW(n(sub.o), dOut, np.zeros((C, C), np.uint16), threads=16)
-    assert bf_err(to_np(sub.dWp), rWp)[0] == 0
-    assert bf_err(n(sub.dO), O.projBackwarddX(dOut, Wp, threads=16))[0] == 0
-    rD = O.compute_d(q4(n(sub.dO)), q4(n(sub.o)))
-    assert np.array_equal(to_np(sub.Dv), rD)
-    rQ, rK, rV = O.backward(q4(n(sub.dO)), rD, to_np(sub.lse), q4(n(sub.q)), q4(n(sub.k)), q4(n(sub.v)),
-                            O.opts(threads=16))
-    for g, r in ((sub.dQ, rQ), (sub.dK, rK), (sub.dV, rV)):
-        a, b = f32(n(g)), f32(r.reshape(R, C))
-        assert float(np.abs(a - b).max() / np.abs(b).max()) <= 2e-2
-    rX = O.computeGradDx(np.zeros((R, C), np.float32), Wq, Wk, Wv, n(sub.dQ), n(sub.dK), n(sub.dV), threads=16)
-    assert f32_err(n(sub.dX), rX) <= 1e-4
-    rQw, rKw, rVw = O.computeGradDw(X, n(sub.dQ), n(sub.dK), n(sub.dV), np.zeros((C, C), np.float32),
-                                    np.zeros((C, C), np.uint16), np.zeros((C, C), np.uint16), threads=16)
-    assert f32_err(to_np(sub.dWq), rQw) <= 1e-4
-    assert bf_err(to_np(sub.dWk), rKw)[0] == 0
-    assert bf_err(to_np(sub.dWv), rVw)[0] == 0
+    return sub, dOut
+
+
+def test_config4_sublayer_chain(gpu, S):
+    """Config 4's sublayer (C=768, H=12, D=64, T=2048) at B=1: the model.h launch sequence on the GPU;
+    every stage checked against the oracle on the GPU's own inputs to that stage (attention by the
+    bars of the attention parity tests)."""
+    sub, dOut = _run_chain(S, gpu, 1, 2048, 12, 768, 4)
+    check_sublayer(sub, dOut, batches=[0], label="config4 B=1")
+
+
+def test_config4_full_size(gpu, S):
+    """Config 4 at its real size, B=8, T=2048, C=768, H=12: R = 16384
+    rows, so the weight gradients run 16 row chunks per product (32 partials for dQw) and the
+    attention backward the XCD-grouped path (96 pairs). Row-local stages are checked on batches 0
+    and 7, the weight gradients over all rows; the phase encoder on the same inputs must give
+    the per-call chain's results bit for bit."""
+    import torch
+    B, T, H, C = 8, 2048, 12, 768
+    print(f"case config4 B={B} T={T} H={H} C={C}", flush=True)
+    S.reserve(S.params_of(torch.empty((B, T, C)), H))  # scratch sized once: the calls below do not allocate
+    sub, dOut = _run_chain(S, gpu, B, T, H, C, 8)
+    check_sublayer(sub, dOut, batches=[0, 7], label="config4 B=8")
+    enc = S.Sublayer(sub.X, sub.Wq, sub.Wk, sub.Wv, sub.Wp, H=H)
+    enc.dOut.copy_(to_gpu(dOut.reshape(B, T, C), gpu))
+    enc.encode(0)
+    enc.encode(1)
+    torch.cuda.synchronize()
+    for n in ("q", "k", "v", "o", "lse", "out", "dO", "Dv", "dQ", "dK", "dV", "dX", "dWq", "dWk", "dWv", "dWp"):
+        assert torch.equal(getattr(sub, n), getattr(enc, n)), n
