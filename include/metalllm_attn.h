@@ -106,6 +106,20 @@ int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const fl
                                     void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
                                     metalllm_stream_t stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The same computation as
+ * flashAttentionBackwardWorkspace (same kernels, bit-identical dQ, dK, dV; dQ written in full),
+ * with the dS tiles in a fixed per-device array of METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64 MiB,
+ * held by every GPU the library runs on until the process ends) instead of a caller workspace.
+ * Calls no hipMalloc/hipFree. Shapes whose metalllmAttnBackwardWorkspaceSize exceeds the array
+ * return METALLLM_ATTN_E_SIZE (config 1, B = 128, NH = 6, M = 256, needs 60 MiB). All calls on
+ * one GPU share the array: calls that overlap on one GPU race. The first call on a device looks
+ * up the array's address there. */
+#define METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
+                                  const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
+                                  const AttentionParams* p, metalllm_stream_t stream);
+
 /* ---- The sublayer around the attention core (attention.metal:19-53, 301-455) ----
  * Plain GEMMs with the reference kernels' names and buffer order. Row-major: X, attn_out (O), dZ,
  * q, k, v, dK, dV, dAttn, out are bf16 [B*M, N]; dQ and dX are fp32 [B*M, N]; weights (q_w, k_w,

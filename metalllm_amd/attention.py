@@ -30,7 +30,8 @@ EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "meta
             "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize", "residualAdd",
             "layernormForward", "layernormBackward",
             "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy",
-            "metalllmSublayerReserve")
+            "metalllmSublayerReserve", "flashAttentionBackwardNoAlloc")
+NOALLOC_SCRATCH_BYTES = 64 << 20  # METALLLM_ATTN_NOALLOC_SCRATCH_BYTES
 
 
 class AttentionParams(ctypes.Structure):
@@ -67,8 +68,10 @@ def _lib():
         L.metalllmAttnBackwardPart.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u64, pp, vp]
         L.flashAttentionBackwardWorkspace.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u64, pp, vp]
         L.metalllmAttnBackwardWorkspaceSize.argtypes = [pp, ctypes.POINTER(u64)]
+        L.flashAttentionBackwardNoAlloc.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, pp, vp]
         for f in (L.flashAttentionForward, L.computeD, L.flashAttentionBackward, L.metalllmAttnBackwardPart,
-                  L.flashAttentionBackwardWorkspace, L.metalllmAttnBackwardWorkspaceSize):
+                  L.flashAttentionBackwardWorkspace, L.metalllmAttnBackwardWorkspaceSize,
+                  L.flashAttentionBackwardNoAlloc):
             f.restype = ctypes.c_int
         L.metalllmAttnErrorString.argtypes = [ctypes.c_int]
         L.metalllmAttnErrorString.restype = ctypes.c_char_p
@@ -155,6 +158,16 @@ def flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, workspace, st
     _check(_lib().flashAttentionBackwardWorkspace(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
                                                   _ptr(dK), _ptr(dV), wp, wn, ctypes.byref(p), _stream(stream)),
            "flashAttentionBackwardWorkspace")
+
+
+def flashAttentionBackwardNoAlloc(dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None):
+    """flashAttentionBackwardWorkspace with the dS tiles in the library's fixed 64 MiB per-device
+    array: allocates nothing; calls overlapping on one GPU race; shapes whose tiles exceed the
+    array raise (E_SIZE)."""
+    p = params or _shape(q)
+    _check(_lib().flashAttentionBackwardNoAlloc(_ptr(dZ), _ptr(d), _ptr(l), _ptr(q), _ptr(k), _ptr(v), _ptr(dQ),
+                                                _ptr(dK), _ptr(dV), ctypes.byref(p), _stream(stream)),
+           "flashAttentionBackwardNoAlloc")
 
 
 def backward_part(part: int, dZ, d, l, q, k, v, dQ, dK, dV, stream=None, params: AttentionParams | None = None,

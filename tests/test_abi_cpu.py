@@ -110,6 +110,21 @@ def test_error_strings():
     assert lib.metalllmAttnErrorString(-9) != lib.metalllmAttnErrorString(-100)
 
 
+def test_no_alloc_backward_validates_before_device():
+    """flashAttentionBackwardNoAlloc rejects shapes whose dS tiles exceed its fixed array, bad
+    shapes, NULL and misaligned pointers before touching the device."""
+    lib = M.library()
+    f = lib.flashAttentionBackwardNoAlloc
+    ok = ctypes.c_void_p(1 << 20)
+    fits = AttentionParams.of(128, 256, 6, 64)      # config 1: 60 MiB of dS tiles
+    too_big = AttentionParams.of(32, 1024, 12, 64)  # config 2: 792 MiB
+    assert f(*([ok] * 9), ctypes.byref(too_big), None) == -5
+    assert f(*([ok] * 9), ctypes.byref(AttentionParams.of(1, 100, 1, 64)), None) == -2
+    assert f(*([ok] * 8), None, ctypes.byref(fits), None) == -1
+    assert f(*([ok] * 8), ctypes.c_void_p((1 << 20) + 2), ctypes.byref(fits), None) == -6
+    assert M.workspace_bytes(128, 256, 6, 64) <= M.attention.NOALLOC_SCRATCH_BYTES < M.workspace_bytes(32, 1024, 12, 64)
+
+
 def test_sublayer_reserve_validates_before_device():
     """metalllmSublayerReserve rejects shapes the sublayer cannot run before touching the device."""
     lib = M.library()

@@ -1,0 +1,50 @@
+"""flashAttentionBackwardNoAlloc (no counterpart in the reference; for callers that cannot
+allocate) through the C ABI against flashAttentionBackwardWorkspace, the entry point whose kernels
+it shares: dQ, dK and dV bit-identical, on two calls in a row, the second with a smaller input
+(the fixed per-device dS array keeps the first call's tiles; every tile the second call reads it
+writes first). Outputs start filled with NaN: the entry point writes them in full."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.attn_case import make_inputs, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, B, T, H, D, seed):
+    import torch
+    import metalllm_amd as M
+    print(f"case B={B} T={T} H={H} D={D} seed={seed}", flush=True)
+    q, k, v, g = (to_gpu(x, gpu) for x in make_inputs(B, T, H, D, seed))
+    out, lse = M.attention_forward(q, k, v)
+    Dv = torch.empty((B, H, T), dtype=torch.float32, device=gpu)
+    M.computeD(g, out, Dv)
+    ws = torch.empty((M.workspace_bytes(B, T, H, D),), dtype=torch.uint8, device=gpu)
+    ref = [torch.full((B, T, H, D), float("nan"), dtype=torch.float32, device=gpu),
+           torch.full_like(q, float("nan")), torch.full_like(q, float("nan"))]
+    M.flashAttentionBackwardWorkspace(g, Dv, lse, q, k, v, *ref, ws)
+    got = [torch.full_like(t, float("nan")) for t in ref]
+    lib = M.library()
+    p = M.AttentionParams.of(B, T, H, D)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = lib.flashAttentionBackwardNoAlloc(ptr(g), ptr(Dv), ptr(lse), ptr(q), ptr(k), ptr(v), *(ptr(t) for t in got),
+                                           ctypes.byref(p), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+
+
+def test_no_alloc_backward_matches_workspace_backward(gpu):
+    # config 1 (60 MiB of dS tiles, near the 64 MiB array), then a smaller D = 128 input
+    _run(gpu, 128, 256, 6, 64, 61)
+    _run(gpu, 2, 512, 4, 128, 62)
+    import metalllm_amd as M
+    with pytest.raises(M.AttentionError):  # tiles beyond the array: rejected before the device
+        import torch
+        x = torch.empty((32, 1024, 12, 64), dtype=torch.bfloat16, device=gpu)
+        d = torch.empty((32, 12, 1024), dtype=torch.float32, device=gpu)
+        dq = torch.empty((32, 1024, 12, 64), dtype=torch.float32, device=gpu)
+        M.flashAttentionBackwardNoAlloc(x, d, d, x, x, x, dq, x, x)
