@@ -70,7 +70,7 @@ struct DiagTag {
 };
 
 // D = 64: three workgroups per CU (168 VGPRs, a few spilled outside the product loop), 6-8%
-// faster than two; D = 128 needs its 244-249 VGPRs and runs two.
+// faster than two; D = 128 needs its 244-253 VGPRs and runs two.
 template <int D, bool DS>
 __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
@@ -144,11 +144,13 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
       dma16_v(src, dst + C::STAT);
     }
   };
-  // lse -> lse*log2(e) in place, by wave 0 once its copy has landed (exponents are base 2)
+  // lse -> lse*log2(e) in place (exponents are base 2) and, for D = 128, D -> D*scale, by wave 0
+  // once its copy has landed
   auto scale_lse = [&](int stage) {
     if (wave == 0) {
       float* l2 = (float*)(smem + stage * C::STAGE + C::STAT);
       l2[lane] = l2[lane] * kLog2e;
+      if (D != 64) l2[64 + lane] = l2[64 + lane] * a.scale;
     }
   };
 
@@ -281,20 +283,24 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
       round_pair(y, r);
       // D = 64: scale = 1/8 is a power of two, so bf16(v * scale) = bf16(v) / 8 exactly (above the
       // subnormal range); dS is carried times 8 and dK, and dQ from the stored dS, are scaled once
-      // when they are stored
-      const float d0 = D == 64 ? x[r] * (y[r] - d0_) : (x[r] * (y[r] - d0_)) * scale;
-      const float d1 = D == 64 ? x[r + 1] * (y[r + 1] - d1_) : (x[r + 1] * (y[r + 1] - d1_)) * scale;
+      // when they are stored. D = 128: p * (dP*scale - D*scale) with D*scale precomputed (one fma
+      // for the reference's subtraction and multiply, :284; the fp32 value differs from
+      // (p*(dP - D))*scale by a few fp32 ulps, below the bf16 rounding that follows)
+      const float d0 = D == 64 ? x[r] * (y[r] - d0_) : x[r] * fmaf(y[r], scale, -d0_);
+      const float d1 = D == 64 ? x[r + 1] * (y[r + 1] - d1_) : x[r + 1] * fmaf(y[r + 1], scale, -d1_);
       uint32_t pk = pack_bf16(d0, d1);
       pin(pk);
       dS[8 * t + u] = pk;
     };
 
     // operand reads run ahead(i) products ahead: four during the first S segment (almost no
-    // vector work there to cover the LDS latency), one afterwards; statistics one slot ahead
+    // vector work there to cover the LDS latency), then two at D = 128 and one at D = 64; the
+    // statistics SA slots ahead (D = 64 has no registers for more at three workgroups per CU)
     constexpr int RING = 5;
-    auto ahead = [](int i) { return i < C::KC ? 4 : 1; };
+    constexpr int SA = D == 128 ? 2 : 1;  // statistics lookahead (slots)
+    auto ahead = [](int i) { return i < C::KC ? 4 : (D == 128 ? 2 : 1); };
     u32x4 ring[RING];
-    f32x4 sring[2];
+    f32x4 sring[SA + 1];
 #pragma unroll
     for (int k = 0; k <= ahead(0); ++k) ring[k] = operand(k);
     sring[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -303,7 +309,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int k = (i ? i - 1 + ahead(i - 1) : ahead(0)) + 1; k <= i + ahead(i) && k < NS; ++k)
         ring[k % RING] = operand(k);
-      if (i + 1 < NS && work(i + 1).kind) sring[(i + 1) % 2] = stats(i + 1);
+      if (i + SA < NS && work(i + SA).kind) sring[(i + SA) % (SA + 1)] = stats(i + SA);
       const u32x4& op = ring[i % RING];
       if (i < 4 * C::KC) {
         const int seg = i / C::KC, c = i % C::KC;
@@ -318,7 +324,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
       }
       // vector work of this slot
       const Work w = work(i);
-      const f32x4 st = sring[i % 2];
+      const f32x4 st = sring[i % (SA + 1)];
 #pragma unroll
       for (int v = 0; v < w.cnt; ++v) {
         if (w.kind == 1)
@@ -340,6 +346,10 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
         if (n >= 1 && j == 1) pack_pairs(n - 1, 0, 8);
         if (n + 1 < 2 * C::DT && n >= 1 && j >= 2) unpack_pairs(n + 1, 4 * (j - 2), 4 * (j - 2) + 4);
       }
+      // D = 128: raised issue priority while S and dP are computed (their chains have little
+      // vector work of their own; the other wave on the SIMD issues its vector work around them)
+      if (D == 128 && i == 0) __builtin_amdgcn_s_setprio(1);
+      if (D == 128 && i + 1 == 4 * C::KC) __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
     }
   };

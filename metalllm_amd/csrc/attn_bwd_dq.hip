@@ -129,6 +129,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   }
   const float lse2 = wave_active ? a.lse[(size_t)pair * a.T + q] * kLog2e : 0.0f;  // exponent in base 2
   const float dq = wave_active ? a.Dv[(size_t)pair * a.T + q] : 0.0f;
+  const float dq_scaled = dq * a.scale;  // D = 128: dS = bf16(p * fma(dP, scale, -D*scale))
   const float sl = a.scale * kLog2e;
   const float scale = a.scale;
 
@@ -235,13 +236,14 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
         db[u] = pack_bf16(y[r], y[r + 1]);
         pin(pa[u], pb[u]);
         pin(db[u]);
-      } else if (st == 2) {  // p * (dP - D)
-        ya[u] = pa[u] * (bf_lo(db[u]) - dq);
-        yb[u] = pb[u] * (bf_hi(db[u]) - dq);
+      } else if (st == 2) {  // p * (dP - D) (D = 64), p * (dP*scale - D*scale) (D = 128)
+        ya[u] = D == 64 ? pa[u] * (bf_lo(db[u]) - dq) : pa[u] * fmaf(bf_lo(db[u]), scale, -dq_scaled);
+        yb[u] = D == 64 ? pb[u] * (bf_hi(db[u]) - dq) : pb[u] * fmaf(bf_hi(db[u]), scale, -dq_scaled);
         pin(ya[u], yb[u]);
-      } else {  // dS = bf16(p * (dP - D) * scale); at D = 64 (scale 1/8, a power of two) dS is
-                // carried times 8 and dQ divided once when it is stored: exact above the subnormals
-        uint32_t pk = D == 64 ? pack_bf16(ya[u], yb[u]) : pack_bf16(ya[u] * scale, yb[u] * scale);
+      } else {  // dS = bf16(.); at D = 64 (scale 1/8, a power of two) dS is carried times 8 and dQ
+                // divided once when it is stored: exact above the subnormals. At D = 128 the same
+                // value as the dK/dV kernel's dS (attn_bwd.hip)
+        uint32_t pk = pack_bf16(ya[u], yb[u]);
         pin(pk);
         dS[u] = pk;
       }
