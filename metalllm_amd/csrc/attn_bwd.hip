@@ -263,7 +263,8 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
     };
     auto p_pair = [&](f32x16& x, int t, int u, float l0, float l1) {
       const int r = 2 * u;
-      round_pair(x, r);
+      x[r] = round_bf16(x[r]);
+      x[r + 1] = round_bf16(x[r + 1]);
       float p0 = exp2_hw(fmaf(x[r], sl, -l0));
       float p1 = exp2_hw(fmaf(x[r + 1], sl, -l1));
       if (DIAG) {
@@ -280,7 +281,8 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
     };
     auto ds_pair = [&](const f32x16& x, f32x16& y, int t, int u, float d0_, float d1_) {
       const int r = 2 * u;
-      round_pair(y, r);
+      y[r] = round_bf16(y[r]);
+      y[r + 1] = round_bf16(y[r + 1]);
       // D = 64: scale = 1/8 is a power of two, so bf16(v * scale) = bf16(v) / 8 exactly (above the
       // subnormal range); dS is carried times 8 and dK, and dQ from the stored dS, are scaled once
       // when they are stored. D = 128: p * (dP*scale - D*scale) with D*scale precomputed (one fma

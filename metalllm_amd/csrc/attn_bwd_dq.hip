@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
     };
 #pragma unroll
     for (int i = 0; i <= ahead(0); ++i) ring[i] = op_of(i);
-    uint32_t sb[16], db[16];
+    float da[16], db[16];  // bf16(dP) of the pairs, as fp32 values
     float ta[16], tb[16], pa[16], pb[16], ya[16], yb[16];
     // vector stage st of pair p of half t (pair index u = 8t + p)
     auto stage = [&](int t, int p, int st) {
@@ -220,9 +220,8 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
       f32x16& y = t ? y1 : y0;
       const int u = 8 * t + p, r = 2 * p;
       if (st == 0) {  // s = bf16(S); exponent argument s*scale*log2e - lse*log2e
-        sb[u] = pack_bf16(x[r], x[r + 1]);
-        ta[u] = fmaf(bf_lo(sb[u]), sl, -lse2);
-        tb[u] = fmaf(bf_hi(sb[u]), sl, -lse2);
+        ta[u] = fmaf(round_bf16(x[r]), sl, -lse2);
+        tb[u] = fmaf(round_bf16(x[r + 1]), sl, -lse2);
         pin(ta[u], tb[u]);
       } else if (st == 1) {  // p = exp2(.), 0 above the diagonal; bf16(dP)
         float p0 = exp2_hw(ta[u]), p1 = exp2_hw(tb[u]);
@@ -233,12 +232,13 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
         }
         pa[u] = p0;
         pb[u] = p1;
-        db[u] = pack_bf16(y[r], y[r + 1]);
+        da[u] = round_bf16(y[r]);
+        db[u] = round_bf16(y[r + 1]);
         pin(pa[u], pb[u]);
-        pin(db[u]);
+        pin(da[u], db[u]);
       } else if (st == 2) {  // p * (dP - D) (D = 64), p * (dP*scale - D*scale) (D = 128)
-        ya[u] = D == 64 ? pa[u] * (bf_lo(db[u]) - dq) : pa[u] * fmaf(bf_lo(db[u]), scale, -dq_scaled);
-        yb[u] = D == 64 ? pb[u] * (bf_hi(db[u]) - dq) : pb[u] * fmaf(bf_hi(db[u]), scale, -dq_scaled);
+        ya[u] = D == 64 ? pa[u] * (da[u] - dq) : pa[u] * fmaf(da[u], scale, -dq_scaled);
+        yb[u] = D == 64 ? pb[u] * (db[u] - dq) : pb[u] * fmaf(db[u], scale, -dq_scaled);
         pin(ya[u], yb[u]);
       } else {  // dS = bf16(.); at D = 64 (scale 1/8, a power of two) dS is carried times 8 and dQ
                 // divided once when it is stored: exact above the subnormals. At D = 128 the same

@@ -76,6 +76,10 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 __device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
+// x rounded to bf16 (nearest even), as an fp32 value: the packed pair (0, x) read as one float.
+// One instruction, where rounding a pair and unpacking both halves takes three.
+__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(pack_bf16(0.0f, x)); }
+
 // Rounds a pair in place to bf16-representable fp32 values.
 __device__ __forceinline__ void round_pair(float& a, float& b) {
   const uint32_t p = pack_bf16(a, b);

@@ -200,11 +200,12 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     constexpr int NM = NSM + NPV;
     // Softmax schedule, software-pipelined over score pairs (p = elements 2p, 2p+1) so that a
     // slot carries independent chains: phase A (stages: A1 mask, running max, bf16(S); for
-    // D=128 also A2 scale, A3 bf16 again) of pair p in slot p/APS + stage; phase B (running max,
+    // D=128 also A2 scale and bf16 again) of pair p in slot p/APS + stage; phase B (running max,
     // factor, rescale flag) in slot BSLOT, right after the last A1; phase C (C1 exponent
     // argument, C2 exp2, C3 row sum and packed P) of pair p in slot BSLOT + 1 + p/CPS + stage.
+    // Each rounding point is one v_cvt_pk_bf16_f32 whose low half is zero, so the register holds
+    // the rounded score as an fp32 value (no unpacking before its next use).
     constexpr int APS = D == 64 ? 2 : 1;
-    constexpr int ANS = D == 64 ? 1 : 3;
     constexpr int BSLOT = 16 / APS;
     constexpr int CPS = D == 64 ? 4 : 2;
     constexpr int LAST = BSLOT + 1 + 15 / CPS + 2;
@@ -230,8 +231,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
     for (int i = 0; i < RING - 1; ++i)
       if (i < NM) ring[i] = operand(i);
     float mxa = -INFINITY, mxb = -INFINITY, ls0 = 0.0f, ls1 = 0.0f, mb = 0.0f;
-    uint32_t X[16], pk1[16];  // bf16 scores of tile kt, pairs (2p, 2p+1)
-    float u0[16], u1[16], t0[16], t1[16], e0[16], e1[16];
+    float r0[16], r1[16];  // bf16-rounded scores of tile kt, pairs (2p, 2p+1), as fp32 values
+    float t0[16], t1[16], e0[16], e1[16];
     // key > q  <=>  off(e) > q - kt*64 - 4h; opaque, so that the compares are not rewritten
     // against 32 loop-invariant bounds
     int dq = q - kt * C::BN - 4 * h;
@@ -267,16 +268,13 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
               mxb = max3f(mxb, a0, a1);
             else
               mxa = max3f(mxa, a0, a1);
-            pk1[p] = pack_bf16(a0, a1);
-            pin(pk1[p]);
-            if (D == 64) X[p] = pk1[p];
+            r0[p] = round_bf16(a0);
+            r1[p] = round_bf16(a1);
+            pin(r0[p], r1[p]);
           } else if (D != 64 && sa == 1) {
-            u0[p] = bf_lo(pk1[p]) * a.scale;
-            u1[p] = bf_hi(pk1[p]) * a.scale;
-            pin(u0[p], u1[p]);
-          } else if (D != 64 && sa == 2) {
-            X[p] = pack_bf16(u0[p], u1[p]);
-            pin(X[p]);
+            r0[p] = round_bf16(r0[p] * a.scale);
+            r1[p] = round_bf16(r1[p] * a.scale);
+            pin(r0[p], r1[p]);
           }
         }
         if (i == BSLOT) {
@@ -297,8 +295,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
         for (int p = 0; p < 16; ++p) {
           const int sc = i - (BSLOT + 1 + p / CPS);  // phase C stage of pair p in this slot
           if (sc == 0) {
-            t0[p] = fmaf(bf_lo(X[p]), c1, -mb);
-            t1[p] = fmaf(bf_hi(X[p]), c1, -mb);
+            t0[p] = fmaf(r0[p], c1, -mb);
+            t1[p] = fmaf(r1[p], c1, -mb);
             pin(t0[p], t1[p]);
           } else if (sc == 1) {
             e0[p] = exp2_hw(t0[p]);
