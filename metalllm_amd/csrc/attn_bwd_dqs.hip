@@ -152,21 +152,34 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
     dsdst[j] = (uint32_t)(C::KBYTES + t * C::DSBYTES + row * 1024);
   }
   const uint32_t smem_a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
-  auto issue = [&](const Item& it, int kt, int stage) {
-    const uint32_t dst = smem_a + stage * C::STAGE;
-    const char* ks = (const char*)(a.k + base_of(it.pair)) + (size_t)kt * 64 * rs * 2;
-#pragma unroll
-    for (int j = 0; j < C::KPW; ++j) dma16(koff[j], ks, dst + 1024 * (wave + C::WAVES * j));
-    // dS tile (qt0 + t, kt); one outside the triangle (or past T) reads the pair's first tile
-    // instead and is never used
-    const char* dsg = (const char*)a.dS + (size_t)it.pair * ntri * 8192;
+  // Copy cursor: the next stage to copy is key tile ktn of item nxt. Its source addresses are
+  // set up once per item (set_cursor) and advanced by one tile per stage, so issuing a stage costs
+  // a few scalar adds (every wave of the CU shares the scalar unit of its SIMD with the others).
+  //   kp       K tile ktn of the item's pair
+  //   dsp[j]   dS tile (qt0 + (wave + WAVES*j)/8, ktn) of the pair's triangle
+  //   qlim[j]  that query tile, or -1 past T: copy j is valid while ktn <= qlim[j]; an invalid one
+  //            reads the pair's first tile (ds0) instead and is never used
+  const size_t ktile = (size_t)64 * rs * 2;
+  const char* kp = nullptr;
+  const char* ds0 = nullptr;
+  const char* dsp[C::DSPW];
+  int qlim[C::DSPW];
+  auto set_cursor = [&](const Item& it) {
+    kp = (const char*)(a.k + base_of(it.pair));
+    ds0 = (const char*)a.dS + (size_t)it.pair * ntri * 8192;
 #pragma unroll
     for (int j = 0; j < C::DSPW; ++j) {
       const int qt = it.qt0 + (wave + C::WAVES * j) / 8;
-      const bool valid = qt < nqt && kt <= qt;
-      const char* src = dsg + (valid ? ((size_t)qt * (qt + 1) / 2 + kt) * 8192 : 0);
-      dma16_nt(dsoff[j], src, dst + dsdst[j]);
+      qlim[j] = qt < nqt ? qt : -1;
+      dsp[j] = ds0 + (qt < nqt ? (size_t)qt * (qt + 1) / 2 * 8192 : 0);
     }
+  };
+  auto issue = [&](int kt, int stage) {
+    const uint32_t dst = smem_a + stage * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::KPW; ++j) dma16(koff[j], kp, dst + 1024 * (wave + C::WAVES * j));
+#pragma unroll
+    for (int j = 0; j < C::DSPW; ++j) dma16_nt(dsoff[j], kt <= qlim[j] ? dsp[j] : ds0, dst + dsdst[j]);
   };
 
   // A = K^T: group g16 covers d 16(g16%2)..+15 of 32-d block m, source lane s16 reads key
@@ -225,17 +238,25 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
       ktn = 0;
       const int mn = list_index(++kn);
       have_next = mn < nlist;
-      if (have_next) nxt = item_at(mn);
+      if (have_next) {
+        nxt = item_at(mn);
+        set_cursor(nxt);
+      }
+    } else {
+      kp += ktile;
+#pragma unroll
+      for (int j = 0; j < C::DSPW; ++j) dsp[j] += 8192;
     }
   };
-  issue(nxt, ktn, 0);
+  set_cursor(nxt);
+  issue(ktn, 0);
   advance_next();
   // Vector-memory operations this wave issued after the copies of the stage awaited next (they
   // complete in issue order): with three stages the copies of the stage after it (c1), and the
   // dQ stores of the previous step (s1) and, with three stages, of the step before (s2).
   bool c1 = false, s1 = false, s2 = false;
   if (C::NSTAGE == 3 && have_next) {
-    issue(nxt, ktn, 1);
+    issue(ktn, 1);
     advance_next();
     c1 = true;
   }
@@ -249,7 +270,7 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
     __syncthreads();  // stage st landed for every wave; every wave is done with the previous stage
     if (C::NSTAGE == 3) c1 = have_next;
     if (have_next) {
-      issue(nxt, ktn, st == 0 ? C::NSTAGE - 1 : st - 1);  // stage (st + NSTAGE - 1) % NSTAGE
+      issue(ktn, st == 0 ? C::NSTAGE - 1 : st - 1);  // stage (st + NSTAGE - 1) % NSTAGE
       advance_next();
     }
     const int qtw = cur.qt0 + wq;
