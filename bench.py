@@ -321,6 +321,52 @@ def main():
     dq_avg = avg(dq_ms)
     rc_kv, rc_dq, rc_bwd = span(2, 3, rc_events), span(3, 4, rc_events), span(2, 4, rc_events)
 
+    if D == 64 and T <= 256:
+        # short sequences: one fused kernel (part 2) computes dK, dV and dQ without the workspace
+        # (part 3 launches nothing); at T = 256 the backward is HBM-bound (5T/16 FLOP per byte)
+        bwd_bytes = 16 * bthd + 8 * B * H * T
+        roofline = {
+            "kernel": "fused short-sequence backward (mla::bwd_short_kernel<false>: dK, dV and dQ)",
+            "bound": "hbm",
+            "achieved": round(bwd_bytes / (kv_avg * 1e-3) / 1e9, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(bwd_bytes / (kv_avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profiles(args.config, "bwd_short"),
+            "algorithmic_bytes": bwd_bytes,
+            "tflops": round(5.0 * unit / (kv_avg * 1e-3) / 1e12, 2),
+            "avg_ms": round(kv_avg, 4),
+        }
+        roofline_dq = None
+    else:
+        roofline = {
+            "kernel": "backward dK/dV kernel with the dS store (mla::bwd_kernel<D, true>)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic_from_profiles(args.config),
+            # the kernel's share of the backward's algorithmic bytes (Q, K, V, dO read; dK, dV
+            # written; lse, D read); the dS tiles it stores for the dQ kernel are design traffic
+            "algorithmic_bytes": 12 * bthd + 8 * B * H * T,
+            "workspace_write_bytes": ws_bytes,
+            "avg_ms": round(kv_avg, 4),
+        }
+        roofline_dq = {
+            "kernel": "backward dQ kernel from the stored dS (mla::dqs_kernel)",
+            "bound": "hbm",
+            "achieved": round(dq_bytes / (dq_avg * 1e-3) / 1e9, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(dq_bytes / (dq_avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profiles(args.config, "dqs"),
+            "algorithmic_bytes": dq_bytes,
+            "note": "bytes this kernel must move (stored dS + K + dQ); the backward's algorithmic bytes "
+                    "(16*BTHD + 8*BHT) do not include the dS round trip",
+            "avg_ms": round(dq_avg, 4),
+        }
+
     result = {
         "metric": "causal attn fwd+bwd TFLOP/s at B,H,T,D bf16; % of MI355X bf16 MFMA peak",
         "value": round(value, 2),
@@ -350,34 +396,10 @@ def main():
             "bwd_tflops": round(fb / (med(bwd_ms) * 1e-3) / 1e12, 2),
             "computeD_gbs": round((4 * bthd + 4 * B * H * T) / (med(cd_ms) * 1e-3) / 1e9, 1),
         },
-        "roofline": {
-            "kernel": "backward dK/dV kernel with the dS store (mla::bwd_kernel<D, true>)",
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic_from_profiles(args.config),
-            # the kernel's share of the backward's algorithmic bytes (Q, K, V, dO read; dK, dV
-            # written; lse, D read); the dS tiles it stores for the dQ kernel are design traffic
-            "algorithmic_bytes": 12 * bthd + 8 * B * H * T,
-            "workspace_write_bytes": ws_bytes,
-            "avg_ms": round(kv_avg, 4),
-        },
-        "roofline_dq": {
-            "kernel": "backward dQ kernel from the stored dS (mla::dqs_kernel)",
-            "bound": "hbm",
-            "achieved": round(dq_bytes / (dq_avg * 1e-3) / 1e9, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(dq_bytes / (dq_avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles(args.config, "dqs"),
-            "algorithmic_bytes": dq_bytes,
-            "note": "bytes this kernel must move (stored dS + K + dQ); the backward's algorithmic bytes "
-                    "(16*BTHD + 8*BHT) do not include the dS round trip",
-            "avg_ms": round(dq_avg, 4),
-        },
+        "roofline": roofline,
     }
+    if roofline_dq is not None:
+        result["roofline_dq"] = roofline_dq
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(B, H, T, D, qk_scale, args.cpu_threads)
     print(json.dumps(result), flush=True)

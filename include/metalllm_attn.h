@@ -79,7 +79,9 @@ int computeD(const uint16_t* dO, const uint16_t* O, float* D, const AttentionPar
  * dZ is dO; d and l are computeD's and the forward's outputs. dQ += gradient (fp32, accumulated
  * into as in the reference: zero it first for the plain gradient); dK, dV = gradients (bf16).
  * Two kernels: dK/dV by key-block owners, then dQ by query-block owners, each recomputing the
- * softmax tile it needs. */
+ * softmax tile it needs. For D = 64 and M <= 256 (the reference's own shape) one kernel does
+ * both: a workgroup per (b, head) keeps the dS tiles in LDS (dK, dV bit-identical to the
+ * two-kernel path). */
 int flashAttentionBackward(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                            const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                            const AttentionParams* p, metalllm_stream_t stream);
@@ -100,7 +102,9 @@ int metalllmAttnBackwardWorkspaceSize(const AttentionParams* p, uint64_t* bytes)
  * what flashAttentionBackward adds into a zeroed dQ up to fp32 summation order. The workspace
  * holds no state between calls, but one
  * workspace must not serve two calls at once. Returns METALLLM_ATTN_E_NULL / _E_ALIGN / _E_SIZE
- * for a NULL, misaligned or too small workspace. No counterpart in the reference. */
+ * for a NULL, misaligned or too small workspace. For D = 64 and M <= 256 it runs the same single
+ * kernel as flashAttentionBackward there (dS stays in LDS; the workspace is validated but not
+ * used). No counterpart in the reference. */
 int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                                     const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                                     void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
@@ -287,7 +291,8 @@ int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g);
  * workspace and part 3 = dQ from the stored dS (flashAttentionBackwardWorkspace is exactly part 2
  * then part 3). Timing the parts separately measures the same work. Same validation and return
  * codes as those entry points (parts 0 and 1 ignore the workspace arguments); a part outside
- * 0..3 returns METALLLM_ATTN_E_LAYOUT. */
+ * 0..3 returns METALLLM_ATTN_E_LAYOUT. For D = 64 and M <= 256 parts 0 and 2 launch the single
+ * fused kernel (part 0 adds dQ, part 2 writes it) and parts 1 and 3 launch nothing. */
 int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                              const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                              void* workspace, uint64_t workspace_bytes, const AttentionParams* p,

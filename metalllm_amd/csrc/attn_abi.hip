@@ -73,6 +73,13 @@ int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const
     if (workspace_bytes < (uint64_t)mla::ds_scratch_bytes(a.B, a.H, a.T)) return METALLLM_ATTN_E_SIZE;
     a.dS = (uint16_t*)workspace;
   }
+  if (mla::backward_is_short(a.T, (int)p->D)) {
+    // one fused kernel computes dK, dV and dQ (part 0 adds dQ, part 2 writes it); parts 1 and 3
+    // have nothing left to do
+    if (part == 1 || part == 3) return METALLLM_ATTN_OK;
+    return mla::launch_backward_short(a, part == 0, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                                         : METALLLM_ATTN_E_LAUNCH;
+  }
   const hipError_t e = part == 0 || part == 2 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
                        : part == 1           ? mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream)
                                              : mla::launch_backward_dqs(a, (int)p->D, (hipStream_t)stream);

@@ -53,6 +53,10 @@ hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
 hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);     // dK, dV (key-owner)
 hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s);  // dQ (query-owner)
 hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s); // dQ from the stored dS
+// Short sequences (D = 64, T <= 256): dK, dV and dQ of a (b,h) pair by one workgroup, one launch,
+// no workspace; dQ added into (accumulate) or written.
+bool backward_is_short(int T, int D);
+hipError_t launch_backward_short(const BwdArgs& a, bool accumulate, hipStream_t s);
 
 // Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
 // spread so that every block of one pair lands on the same XCD (workgroups are handed to the

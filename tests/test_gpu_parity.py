@@ -71,6 +71,8 @@ CASES = [
     (3, 320, 1, 64, 1.0, 16),     # 5 tiles, B*H not a multiple of 8
     (4, 448, 2, 128, 1.0, 17),    # 8 pairs: XCD-affine two-tile dQ ring (T < 512), 7 tiles
     (2, 576, 4, 128, 1.0, 18),    # 8 pairs: XCD-affine four-tile dQ ring, last item 1 of 4 tiles
+    (2, 128, 3, 64, 1.5, 19),     # short-sequence backward (one workgroup per pair), two tiles, peaky
+    (1, 192, 5, 64, 1.0, 20),     # short-sequence backward, three tiles (idle waves in both phases)
 ]
 
 
