@@ -17,7 +17,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmetalllm_attn.so")
 SOURCES = ["attn_abi.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dq.hip", "attn_bwd_dqs.hip", "attn_computed.hip",
-           "attn_noalloc.hip", "sublayer.hip", "glue.hip"]
+           "attn_noalloc.hip", "sublayer.hip", "sublayer_gemm.hip", "glue.hip"]
 LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]  # sublayer GEMMs
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

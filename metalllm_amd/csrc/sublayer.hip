@@ -26,6 +26,12 @@
 
 #include "../../include/metalllm_attn.h"
 
+namespace mla {  // sublayer_gemm.hip
+bool grad_dx_fused_ok(int R, int C);
+hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
+                          const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s);
+}  // namespace mla
+
 namespace {
 
 int validate_gemm(const AttentionParams* p) {
@@ -259,9 +265,16 @@ int op_proj_dx(const Ctx& c, const uint16_t* dZ, const uint16_t* proj_w, uint16_
   return gemm_rm(c, false, true, R, C, C, dZ, BF, C, proj_w, BF, C, 0.0f, dAttn, BF, C);
 }
 
-// hi, lo: the two-term bf16 split of dQ (split_dq)
-int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw,
+// Row and feature counts that are multiples of 128 run the hand-written kernel (sublayer_gemm.hip),
+// which reads the fp32 dQ itself; other shapes use the library on hi, lo, the two-term bf16 split
+// of dQ (split_dq).
+int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
                const uint16_t* hi, const uint16_t* lo, const uint16_t* dK, const uint16_t* dV, int R, int C) {
+  if (mla::grad_dx_fused_ok(R, C)) {
+    if (c.query) return METALLLM_ATTN_OK;
+    return mla::launch_grad_dx(dX, dQ, dK, dV, qw, kw, vw, R, C, c.stream) == hipSuccess ? METALLLM_ATTN_OK
+                                                                                        : METALLLM_ATTN_E_LAUNCH;
+  }
   TRY(gemm_rm(c, false, true, R, C, C, hi, BF, C, qw, BF, C, 1.0f, dX, F32, C));
   TRY(gemm_rm(c, false, true, R, C, C, lo, BF, C, qw, BF, C, 1.0f, dX, F32, C));
   TRY(gemm_rm(c, false, true, R, C, C, dK, BF, C, kw, BF, C, 1.0f, dX, F32, C));
@@ -374,9 +387,10 @@ int computeGradDx(float* dX, const uint16_t* qw, const uint16_t* kw, const uint1
   const size_t e = (size_t)R * C;
   Public u(stream);
   TRY(u.s.rc);
+  if (mla::grad_dx_fused_ok(R, C)) return op_grad_dx(u.c, dX, qw, kw, vw, dQ, nullptr, nullptr, dK, dV, R, C);
   TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e, u.c.stream));
   TRY(split_dq(u.c, dQ, e, u.s.st->split));
-  return op_grad_dx(u.c, dX, qw, kw, vw, u.s.st->split, u.s.st->split + e, dK, dV, R, C);
+  return op_grad_dx(u.c, dX, qw, kw, vw, dQ, u.s.st->split, u.s.st->split + e, dK, dV, R, C);
 }
 
 int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
@@ -473,7 +487,7 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
                                         attn_ws_bytes, p, s));
   }
   TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
-  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, split, split + e, b->dK, b->dV, R, C));
+  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, split + e, b->dK, b->dV, R, C));
   TRY(op_grad_dw(c, b->X, split, split + e, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
   if (c.query) return METALLLM_ATTN_OK;
   if (block) {  // model.h:692-695
