@@ -10,15 +10,18 @@
 // Row-major matrices: X, O, dZ, Q, K, V, dK, dV bf16 [R, C] and dQ, dX fp32 [R, C] with R = B*M rows
 // and C = N = NH*D features; weights bf16 [C, C] indexed [input feature][output feature].
 //
-// These are plain GEMMs (no fused epilogue), so they run on the platform library: rocBLAS
-// gemm_ex with bf16 operands, fp32 accumulation and a bf16 or fp32 destination (beta = 1 for the
-// reference's multiply_accumulate kernels: the destination is read once and the sum rounded once).
-// The one operand the library cannot take as is, the fp32 dQ read by computeGradDx/Dw, is split by
-// a HIP kernel into two bf16 terms, dQ = hi + lo + O(2^-16 |dQ|), and each product runs twice:
-// the fp32 dQ never makes a bf16 round trip of its own.
+// The bf16 GEMMs run on the platform library: rocBLAS gemm_ex with bf16 operands, fp32
+// accumulation and a bf16 or fp32 destination (beta = 1 for the reference's multiply_accumulate
+// kernels: the destination is read once and the sum rounded once). computeGradDx and computeGradDw
+// read the fp32 dQ, which the library cannot take as is: for row and feature counts that are
+// multiples of 128 they run hand-written matrix-core kernels (sublayer_gemm.hip) that load dQ as
+// fp32 and split it in registers into two bf16 terms, dQ = hi + lo + O(2^-16 |dQ|), each product
+// running on both; for other shapes a HIP kernel writes the same split to memory (split_dq) and
+// the library runs each product twice. Either way the fp32 dQ never makes a bf16 round trip.
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <initializer_list>
 #include <mutex>
 #include <utility>
@@ -30,6 +33,10 @@ namespace mla {  // sublayer_gemm.hip
 bool grad_dx_fused_ok(int R, int C);
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
                           const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s);
+bool grad_dw_fused_ok(int R, int C);
+size_t grad_dw_partial_floats(int R, int C);
+hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
+                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, hipStream_t s);
 }  // namespace mla
 
 namespace {
@@ -188,6 +195,19 @@ int row_chunks(int R) {
   return 1;
 }
 
+// Elements of the dQ split (hi, then lo) that the library paths of computeGradDx and
+// computeGradDw read: none when the hand-written kernels take the shape (they split in registers).
+size_t split_need(int R, int C) {
+  return mla::grad_dx_fused_ok(R, C) && mla::grad_dw_fused_ok(R, C) ? 0 : 2 * (size_t)R * C;
+}
+
+// fp32 partial floats for projBackwarddW (row_chunks(R) products of C x C) and computeGradDw (the
+// hand-written kernel's chunks, or twice row_chunks(R) for the library path).
+size_t partial_need(int R, int C) {
+  const size_t lib = (size_t)row_chunks(R) * C * C;
+  return mla::grad_dw_fused_ok(R, C) ? std::max(lib, mla::grad_dw_partial_floats(R, C)) : 2 * lib;
+}
+
 int xt_g_partials(const Ctx& c, const uint16_t* X, const uint16_t* G, int R, int C, int parts, float* out) {
   const float alpha = 1.0f, beta = 0.0f;
   const int Rs = R / parts;
@@ -281,9 +301,18 @@ int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, 
   return gemm_rm(c, false, true, R, C, C, dV, BF, C, vw, BF, C, 1.0f, dX, F32, C);
 }
 
-// partial: at least 2 * row_chunks(R) * C * C floats
-int op_grad_dw(const Ctx& c, const uint16_t* x, const uint16_t* hi, const uint16_t* lo, const uint16_t* dK,
-               const uint16_t* dV, float* dQw, uint16_t* dKw, uint16_t* dVw, int R, int C, float* part) {
+// partial: at least partial_need(R, C) floats. Row counts that are multiples of 128 and feature
+// counts that are multiples of 128 run the hand-written kernel (sublayer_gemm.hip) on the fp32 dQ;
+// other shapes use the library on hi, lo, the two-term bf16 split of dQ (split_dq).
+int op_grad_dw(const Ctx& c, const uint16_t* x, const float* dQ, const uint16_t* hi, const uint16_t* lo,
+               const uint16_t* dK, const uint16_t* dV, float* dQw, uint16_t* dKw, uint16_t* dVw, int R, int C,
+               float* part) {
+  if (mla::grad_dw_fused_ok(R, C)) {
+    if (c.query) return METALLLM_ATTN_OK;
+    return mla::launch_grad_dw(x, dQ, dK, dV, dQw, dKw, dVw, part, R, C, c.stream) == hipSuccess
+               ? METALLLM_ATTN_OK
+               : METALLLM_ATTN_E_LAUNCH;
+  }
   const int parts = row_chunks(R);
   const size_t cc = (size_t)C * C;
   // dQw: the partials of X^T.hi and X^T.lo together, added into dQw once
@@ -366,7 +395,7 @@ int projBackwarddW(const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProj
   const int R = (int)(p->B * p->M), C = (int)p->N;
   Public u(stream);
   TRY(u.s.rc);
-  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, (size_t)row_chunks(R) * C * C, u.c.stream));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, partial_need(R, C), u.c.stream));
   return op_proj_dw(u.c, attn_out, dZ, dProjw, R, C, u.s.st->partial);
 }
 
@@ -401,10 +430,12 @@ int computeGradDw(const uint16_t* x, const float* dQ, const uint16_t* dK, const 
   const size_t e = (size_t)R * C;
   Public u(stream);
   TRY(u.s.rc);
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, partial_need(R, C), u.c.stream));
+  if (mla::grad_dw_fused_ok(R, C))
+    return op_grad_dw(u.c, x, dQ, nullptr, nullptr, dK, dV, dQw, dKw, dVw, R, C, u.s.st->partial);
   TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * e, u.c.stream));
-  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, u.c.stream));
   TRY(split_dq(u.c, dQ, e, u.s.st->split));
-  return op_grad_dw(u.c, x, u.s.st->split, u.s.st->split + e, dK, dV, dQw, dKw, dVw, R, C, u.s.st->partial);
+  return op_grad_dw(u.c, x, dQ, u.s.st->split, u.s.st->split + e, dK, dV, dQw, dKw, dVw, R, C, u.s.st->partial);
 }
 
 }  // extern "C"
@@ -486,9 +517,15 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
     TRY(flashAttentionBackwardWorkspace(b->dAttn, b->Dsum, b->l, b->q, b->k, b->v, b->dQ, b->dK, b->dV, attn_ws,
                                         attn_ws_bytes, p, s));
   }
-  TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
-  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, split + e, b->dK, b->dV, R, C));
-  TRY(op_grad_dw(c, b->X, split, split + e, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
+  uint16_t* lo = nullptr;  // no split when both hand-written kernels take the shape
+  if (split_need(R, C)) {
+    TRY(split_dq(c, b->dQ, e, split));  // one split serves both consumers
+    lo = split + e;
+  } else {
+    split = nullptr;
+  }
+  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C));
+  TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
   if (c.query) return METALLLM_ATTN_OK;
   if (block) {  // model.h:692-695
     TRY(castFloatToBfloat(b->dX, b->dStream, (uint32_t)e, s));
@@ -507,12 +544,12 @@ int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, cons
     return METALLLM_ATTN_E_LIBRARY;
   }
   if (g->phase == 1) {
-    if (hipMalloc((void**)&g->split, 2 * (size_t)R * C * sizeof(uint16_t)) != hipSuccess) g->split = nullptr;
-    if (hipMalloc((void**)&g->partial, 2 * (size_t)row_chunks(R) * C * C * sizeof(float)) != hipSuccess)
-      g->partial = nullptr;
+    const size_t split = split_need(R, C);
+    if (split && hipMalloc((void**)&g->split, split * sizeof(uint16_t)) != hipSuccess) g->split = nullptr;
+    if (hipMalloc((void**)&g->partial, partial_need(R, C) * sizeof(float)) != hipSuccess) g->partial = nullptr;
     TRY(metalllmAttnBackwardWorkspaceSize(p, &g->attn_ws_bytes));
     if (hipMalloc(&g->attn_ws, g->attn_ws_bytes) != hipSuccess) g->attn_ws = nullptr;
-    if (!g->split || !g->partial || !g->attn_ws) return METALLLM_ATTN_E_LIBRARY;
+    if ((split && !g->split) || !g->partial || !g->attn_ws) return METALLLM_ATTN_E_LIBRARY;
   }
   // the workspace the phase's rocBLAS calls need, owned by the graph
   size_t ws = 0;
@@ -556,8 +593,8 @@ int metalllmSublayerEncode(int phase, const metalllmSublayerBuffers* b, const At
   TRY(u.s.rc);
   uint64_t ws = 0;
   if (phase == 1) {
-    TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C, u.c.stream));
-    TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, u.c.stream));
+    TRY(ensure(u.s.st->split, u.s.st->split_elems, split_need(R, C), u.c.stream));
+    TRY(ensure(u.s.st->partial, u.s.st->partial_elems, partial_need(R, C), u.c.stream));
     TRY(metalllmAttnBackwardWorkspaceSize(p, &ws));
     TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws, u.c.stream));
   }
@@ -573,8 +610,8 @@ int metalllmSublayerReserve(const AttentionParams* p) {
   TRY(metalllmAttnBackwardWorkspaceSize(p, &ws));
   Public u(nullptr);
   TRY(u.s.rc);
-  TRY(ensure(u.s.st->split, u.s.st->split_elems, 2 * (size_t)R * C, nullptr));
-  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, 2 * (size_t)row_chunks(R) * C * C, nullptr));
+  TRY(ensure(u.s.st->split, u.s.st->split_elems, split_need(R, C), nullptr));
+  TRY(ensure(u.s.st->partial, u.s.st->partial_elems, partial_need(R, C), nullptr));
   TRY(ensure(u.s.st->attn_ws, u.s.st->attn_ws_bytes, (size_t)ws, nullptr));
   return METALLLM_ATTN_OK;
 }

@@ -1,17 +1,18 @@
-// sublayer_gemm.hip -- hand-written matrix-core kernel for computeGradDx
-// (/root/reference/attention.metal:301-341):
-//   dX += dQ.Wq^T + dK.Wk^T + dV.Wv^T
-// with dQ fp32, dK and dV bf16 [R, C], weights bf16 [C, C] indexed [input feature][output
-// feature] and dX fp32 [R, C] (read once, written once).
+// sublayer_gemm.hip -- hand-written matrix-core kernels for the two GEMMs of metalLLM's attention
+// sublayer that read the fp32 dQ:
+//   computeGradDx (/root/reference/attention.metal:301-341)  dX += dQ.Wq^T + dK.Wk^T + dV.Wv^T
+//   computeGradDw (/root/reference/attention.metal:343-383)  dWq += X^T.dQ, dWk += X^T.dK, dWv += X^T.dV
+// with dQ fp32, X, dK and dV bf16 [R, C], weights bf16 [C, C] indexed [input feature][output
+// feature], dX and dWq fp32, dWk and dWv bf16; every destination is read once and written once.
 //
 // The reference reads the fp32 dQ directly (its matmul2d mixes the float dQ with bfloat weights
-// into a float destination). Here the kernel loads dQ as fp32 and splits every element in
+// into a float destination). Here both kernels load dQ as fp32 and split every element in
 // registers into two bf16 terms, hi = bf16(x) and lo = bf16(x - hi) (|x - hi - lo| <= 2^-17 |x|),
-// and runs the product on both: the fp32 gradient reaches the matrix cores without a bf16 round
-// trip and without a separate split pass through HBM. All three products accumulate into one set
-// of fp32 accumulators, so dX is read and written once instead of once per product.
+// and run the product on both: the fp32 gradient reaches the matrix cores without a bf16 round
+// trip and without a separate split pass through HBM.
 //
-// Tiling: a workgroup of 4 waves computes a 128 (rows r) x 128 (features i) tile of dX as
+// computeGradDx: all three products accumulate into one set of fp32 accumulators, so dX is read
+// and written once instead of once per product. Tiling: a workgroup of 4 waves computes a 128 (rows r) x 128 (features i) tile of dX as
 // dX^T = W . G^T (m = i, n = r, k = j): the A operand is a weight row W[i][j..j+7] and the B
 // operand a gradient row G[r][j..j+7], both 16-byte reads from row-major LDS tiles (pitch 72
 // elements: conflict-free 16-byte row reads), and each lane ends with four consecutive i of one
@@ -23,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -190,9 +192,266 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
   }
 }
 
+// ---- computeGradDw (attention.metal:343-383): dWq += X^T.dQ (fp32), dKw += X^T.dK, dVw += X^T.dV
+// (bf16), X bf16 [R, C], dQ fp32, dK and dV bf16 [R, C]; the sums run over all R rows into C x C
+// outputs, too few 128 x 128 tiles to fill the chip, so the rows are split into chunks. A work
+// item is one tile of one weight over one chunk of rows, written as an fp32 partial; dWq items
+// run two products per row (hi and lo of dQ, split in registers as in grad_dx_kernel) over half
+// as many rows, so every item has the same matrix-core work. grad_dw_reduce_kernel then adds the
+// partials and the destination's previous value once and rounds once.
+//
+// Operands: the tile is computed transposed, W^T = G^T . X (m = j, n = i, k = r), so each lane
+// ends with four consecutive j of one i, stored as 16-byte words of the row-major partial. Both
+// operands need 8 rows r of one column per lane: they come from row-major LDS tiles [r][128
+// columns] by ds_read_b64_tr_b16 (pitch 160 elements: the 4 rows x 64 bytes read by 32 lanes of
+// one transposing read fall in distinct banks).
+constexpr int kGwTile = 128;
+constexpr int kGwK = 64;                         // rows r per step
+constexpr int kGwP = kGwTile + 32;               // LDS row pitch (elements)
+constexpr int kGwTileBytes = kGwK * kGwP * 2;    // 20 KB
+
+__device__ __forceinline__ u32x2 lds_tr8(uint32_t a) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(uintptr_t)a));
+}
+
+struct GwShape {
+  int C, nt;        // features, tiles per side
+  int steps;        // R / kGwK
+  int nq, nkv;      // row chunks of dWq, and of each of dKw and dVw
+  int items;        // nt^2 (nq + 2 nkv)
+  int per_xcd;      // items / 8 when 8 divides items, else 0
+};
+
+// Work items in order (weight, chunk, i block, j block): dWq's, then dKw's, then dVw's. Workgroups
+// are dealt to the 8 XCDs in turn (blockIdx % 8), so when 8 divides the item count each XCD takes
+// a contiguous range of items: the items that share a chunk's rows run on one XCD and share its L2.
+__global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
+                                                        const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
+                                                        float* __restrict__ part, GwShape sh) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[3 * kGwTileBytes];  // X, G (dQ hi), dQ lo
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31, g16 = lane >> 4, s16 = lane & 15;
+  const int C = sh.C, tiles = sh.nt * sh.nt;
+  int item = sh.per_xcd ? (int)(blockIdx.x % 8) * sh.per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  int wsel = 0, nch = sh.nq, pbase = 0;
+  if (item >= tiles * sh.nq) {
+    item -= tiles * sh.nq;
+    wsel = 1 + item / (tiles * sh.nkv);
+    item -= (wsel - 1) * tiles * sh.nkv;
+    nch = sh.nkv;
+    pbase = sh.nq + (wsel - 1) * sh.nkv;
+  }
+  const int chunk = item / tiles, tile = item - chunk * tiles;
+  const int i0 = (tile / sh.nt) * kGwTile, j0 = (tile % sh.nt) * kGwTile;
+  const int s0 = (int)((long)chunk * sh.steps / nch), s1 = (int)((long)(chunk + 1) * sh.steps / nch);
+  const uint16_t* G = wsel == 1 ? dK : dV;
+  const int wi = wave & 1, wj = wave >> 1;
+  const uint32_t sX = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
+  const uint32_t sH = sX + kGwTileBytes, sL = sX + 2 * kGwTileBytes;
+
+  // copies of a step's tiles (64 rows): bf16, c = t + 256q, q < 4: row c/16, 16-byte chunk c%16;
+  // fp32 dQ, c = t + 256q, q < 8: row c/32, floats 4(c%32)..+3
+  u32x4 xreg[4], greg[4];
+  f32x4 qreg[8];
+  auto load_x = [&](int r) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      xreg[q] = *(const u32x4*)(X + (size_t)(r + (c >> 4)) * C + i0 + 8 * (c & 15));
+    }
+  };
+  auto load_g = [&](int r) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      greg[q] = *(const u32x4*)(G + (size_t)(r + (c >> 4)) * C + j0 + 8 * (c & 15));
+    }
+  };
+  auto load_q = [&](int r) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = tid + 256 * q;
+      qreg[q] = *(const f32x4*)(dQ + (size_t)(r + (c >> 5)) * C + j0 + 4 * (c & 31));
+    }
+  };
+  auto store_x = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      lds_st16(sX + 2 * ((c >> 4) * kGwP + 8 * (c & 15)), xreg[q]);
+    }
+  };
+  auto store_g = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      lds_st16(sH + 2 * ((c >> 4) * kGwP + 8 * (c & 15)), greg[q]);
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = tid + 256 * q;
+      const f32x4 x = qreg[q];
+      const uint32_t h01 = pack_bf16(x[0], x[1]), h23 = pack_bf16(x[2], x[3]);
+      const uint32_t l01 = pack_bf16(x[0] - bf_lo(h01), x[1] - bf_hi(h01));
+      const uint32_t l23 = pack_bf16(x[2] - bf_lo(h23), x[3] - bf_hi(h23));
+      const uint32_t off = 2 * ((c >> 5) * kGwP + 4 * (c & 31));
+      lds_st8(sH + off, u32x2{h01, h23});
+      lds_st8(sL + off, u32x2{l01, l23});
+    }
+  };
+
+  // transposing reads of a 32-column block: source lane s16 of group g16 addresses row
+  // 4h + s16/4 (+8 for the second read, +16 per k step), column 16(g16%2) + 4(s16%4); the lane
+  // receives column l32 of the block at rows {4h..4h+3, 8+4h..8+4h+3}, the same rows for both
+  // operands
+  const uint32_t tr = 2 * ((4 * h + (s16 >> 2)) * kGwP + 16 * (g16 & 1) + 4 * (s16 & 3));
+  auto tr_op = [&](uint32_t base, int col0, int ks) -> u32x4 {
+    const uint32_t a = base + tr + 2 * (16 * ks * kGwP + col0);
+    const u32x2 lo = lds_tr8(a), hi = lds_tr8(a + 2 * 8 * kGwP);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+  // acc[mj][ni]: W^T block (j = 64 wj + 32 mj, i = 64 wi + 32 ni)
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mj = 0; mj < 2; ++mj)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mj][ni] = zero16();
+  auto compute = [&](auto two_tag) {
+    constexpr bool TWO = decltype(two_tag)::value;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 Bx[2], Ah[2], Al[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        Bx[t] = tr_op(sX, 64 * wi + 32 * t, ks);
+        Ah[t] = tr_op(sH, 64 * wj + 32 * t, ks);
+        if (TWO) Al[t] = tr_op(sL, 64 * wj + 32 * t, ks);
+      }
+#pragma unroll
+      for (int mj = 0; mj < 2; ++mj)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          acc[mj][ni] = mfma(Ah[mj], Bx[ni], acc[mj][ni]);
+          if (TWO) acc[mj][ni] = mfma(Al[mj], Bx[ni], acc[mj][ni]);
+        }
+    }
+  };
+  auto run = [&](auto two_tag) {
+    constexpr bool TWO = decltype(two_tag)::value;
+    load_x(s0 * kGwK);
+    if (TWO) load_q(s0 * kGwK);
+    else load_g(s0 * kGwK);
+    store_x();
+    if (TWO) store_q();
+    else store_g();
+    __syncthreads();
+    for (int s = s0; s < s1; ++s) {
+      const bool more = s + 1 < s1;
+      if (more) {
+        load_x((s + 1) * kGwK);
+        if (TWO) load_q((s + 1) * kGwK);
+        else load_g((s + 1) * kGwK);
+      }
+      compute(two_tag);
+      if (more) {
+        __syncthreads();
+        store_x();
+        if (TWO) store_q();
+        else store_g();
+        __syncthreads();
+      }
+    }
+  };
+  if (wsel == 0) run(std::true_type{});
+  else run(std::false_type{});
+
+  // lane: i = i0 + 64 wi + 32 ni + l32, j = j0 + 64 wj + 32 mj + 8g + 4h + (0..3)
+  float* dst = part + (size_t)(pbase + chunk) * C * C;
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni) {
+    float* row = dst + (size_t)(i0 + 64 * wi + 32 * ni + l32) * C + j0 + 64 * wj + 4 * h;
+#pragma unroll
+    for (int mj = 0; mj < 2; ++mj)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(f32x4*)(row + 32 * mj + 8 * g) =
+            f32x4{acc[mj][ni][4 * g], acc[mj][ni][4 * g + 1], acc[mj][ni][4 * g + 2], acc[mj][ni][4 * g + 3]};
+  }
+}
+
+// dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw = bf16(previous + the sum of
+// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread.
+__global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __restrict__ part, float* __restrict__ dQw,
+                                                               uint16_t* __restrict__ dKw, uint16_t* __restrict__ dVw,
+                                                               int C, int nq, int nkv) {
+  const size_t cc = (size_t)C * C, n4 = cc / 4;
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < 3 * n4; e += (size_t)gridDim.x * blockDim.x) {
+    const int w = (int)(e / n4);
+    const size_t o = 4 * (e - (size_t)w * n4);
+    const int p0 = w == 0 ? 0 : nq + (w - 1) * nkv, np = w == 0 ? nq : nkv;
+    f32x4 acc = *(const f32x4*)(part + (size_t)p0 * cc + o);
+    for (int p = 1; p < np; ++p) acc += *(const f32x4*)(part + (size_t)(p0 + p) * cc + o);
+    if (w == 0) {
+      f32x4* d = (f32x4*)(dQw + o);
+      *d = *d + acc;
+    } else {
+      u32x2* d = (u32x2*)((w == 1 ? dKw : dVw) + o);
+      const u32x2 old = *d;
+      *d = u32x2{pack_bf16(bf_lo(old[0]) + acc[0], bf_hi(old[0]) + acc[1]),
+                 pack_bf16(bf_lo(old[1]) + acc[2], bf_hi(old[1]) + acc[3])};
+    }
+  }
+}
+
+GwShape grad_dw_shape(int R, int C, int cus) {
+  GwShape sh;
+  sh.C = C;
+  sh.nt = C / kGwTile;
+  sh.steps = R / kGwK;
+  const int tiles = sh.nt * sh.nt;
+  // one round of items on two workgroups per CU; dWq chunks are twice as many (half as long)
+  sh.nkv = std::max(1, std::min(2 * cus / (4 * tiles), sh.steps / 2));
+  sh.nq = 2 * sh.nkv;
+  sh.items = tiles * (sh.nq + 2 * sh.nkv);
+  sh.per_xcd = sh.items % 8 == 0 ? sh.items / 8 : 0;
+  return sh;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;
+  return cus;
+}
+
 }  // namespace
 
 bool grad_dx_fused_ok(int R, int C) { return R % kGxTile == 0 && C % kGxTile == 0; }
+
+bool grad_dw_fused_ok(int R, int C) { return R % (2 * kGwK) == 0 && C % kGwTile == 0; }
+
+// Partial floats launch_grad_dw needs for R x C on the current device (the chunk counts follow
+// its compute-unit count).
+size_t grad_dw_partial_floats(int R, int C) {
+  const GwShape sh = grad_dw_shape(R, C, device_cus());
+  return (size_t)(sh.nq + 2 * sh.nkv) * C * C;
+}
+
+hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
+                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, hipStream_t s) {
+  const GwShape sh = grad_dw_shape(R, C, device_cus());
+  hipLaunchKernelGGL(grad_dw_kernel, dim3((unsigned)sh.items), dim3(256), 0, s, X, dQ, dK, dV, partial, sh);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n4 = 3 * (size_t)C * C / 4;
+  hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
+                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv);
+  return hipGetLastError();
+}
 
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
                           const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s) {

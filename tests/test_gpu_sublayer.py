@@ -62,10 +62,13 @@ def test_forward_gemms(gpu, S):
     assert bad == 0
 
 
-@pytest.mark.parametrize("B,T,H,C", [(2, 256, 12, 768), (1, 320, 5, 200)])
+@pytest.mark.parametrize("B,T,H,C", [(2, 256, 12, 768), (1, 384, 3, 384), (1, 320, 5, 200)])
 def test_backward_gemms(gpu, S, B, T, H, C):
-    """R and C multiples of 128 run computeGradDx's hand-written kernel (fp32 dQ split in
-    registers); the second shape runs the library path on the split dQ."""
+    """R and C multiples of 128 run the hand-written computeGradDx and computeGradDw kernels (fp32
+    dQ split in registers); the last shape runs the library path on the split dQ. For
+    computeGradDw, R=512, C=768 gives 432 work items (dealt to the XCDs in contiguous ranges) and
+    R=384, C=384 gives 108 (not a multiple of 8: workgroup order) with dWq chunks of one 64-row
+    step; both are called twice, so the second call accumulates into nonzero destinations."""
     import torch
     R = B * T
     X, (Wq, Wk, Wv, Wp) = inputs(R, C, 2)
@@ -101,14 +104,16 @@ def test_backward_gemms(gpu, S, B, T, H, C):
     dKw = torch.zeros((C, C), dtype=torch.bfloat16, device=gpu)
     dVw = torch.zeros((C, C), dtype=torch.bfloat16, device=gpu)
     S.computeGradDw(g["X"], g["dQ"], g["dK"], g["dV"], dQw, dKw, dVw, p)
+    S.computeGradDw(g["X"], g["dQ"], g["dK"], g["dV"], dQw, dKw, dVw, p)
     rQw, rKw, rVw = O.computeGradDw(X, dQ, dK, dV, np.zeros((C, C), np.float32), np.zeros((C, C), np.uint16),
                                     np.zeros((C, C), np.uint16), threads=16)
+    rQw, rKw, rVw = O.computeGradDw(X, dQ, dK, dV, rQw, rKw, rVw, threads=16)
     e = f32_err(to_np(dQw), rQw)
-    print(f"computeGradDw dQw: rel-to-max {e:.3g}")
+    print(f"computeGradDw x2 dQw: rel-to-max {e:.3g}")
     assert e <= 1e-4
     for name, t, r in (("dKw", dKw, rKw), ("dVw", dVw, rVw)):
         bad, mx = bf_err(to_np(t), r)
-        print(f"computeGradDw {name}: beyond bar {bad}, max err {mx:.3g}")
+        print(f"computeGradDw x2 {name}: beyond bar {bad}, max err {mx:.3g}")
         assert bad == 0
 
 
