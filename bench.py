@@ -173,6 +173,12 @@ def bench_sublayer(args):
     ms_graph = timed(lambda: (graphs[0].launch(stream), graphs[1].launch(stream)))
     for g in graphs:
         g.close()
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
     ms = ms_encode
     result = {
         "metric": "attention sublayer fwd+bwd ms per step (config 4), with the attention share",

@@ -45,12 +45,17 @@ __device__ __forceinline__ void lds_st8(uint32_t a, u32x2 v) { *(__attribute__((
 __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
                                                         const uint16_t* __restrict__ Wq, const uint16_t* __restrict__ Wk,
-                                                        const uint16_t* __restrict__ Wv, int C) {
+                                                        const uint16_t* __restrict__ Wv, int C, int items) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[3 * kGxTileBytes];  // W, G hi, G lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
-  const int r0 = blockIdx.x * kGxTile, i0 = blockIdx.y * kGxTile;
+  // tile order: row block major, feature block minor. Workgroups are dealt to the 8 XCDs in turn
+  // (blockIdx % 8); when 8 divides the tile count each XCD takes a contiguous range of tiles, so
+  // the C/128 tiles that read the same gradient rows run together on one XCD and share its L2.
+  const int nfb = C / kGxTile;
+  const int item = items % 8 == 0 ? (int)(blockIdx.x % 8) * (items / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int r0 = (item / nfb) * kGxTile, i0 = (item % nfb) * kGxTile;
   const int wi = wave & 1, wr = wave >> 1;
   const uint32_t sW = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
   const uint32_t sH = sW + kGxTileBytes, sL = sW + 2 * kGxTileBytes;
@@ -455,8 +460,8 @@ hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK
 
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
                           const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s) {
-  const dim3 grid((unsigned)(R / kGxTile), (unsigned)(C / kGxTile));
-  hipLaunchKernelGGL(grad_dx_kernel, grid, dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C);
+  const int items = (R / kGxTile) * (C / kGxTile);
+  hipLaunchKernelGGL(grad_dx_kernel, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
   return hipGetLastError();
 }
 
