@@ -5,12 +5,12 @@ The product is libmetalllm_attn.so (C ABI in include/metalllm_attn.h); this pack
 """
 from .attention import (AttentionError, AttentionParams, attention_backward, attention_forward, backward_part,
                         computeD, flashAttentionBackward, flashAttentionBackwardNoAlloc, flashAttentionBackwardWorkspace,
-                        flashAttentionForward, library, work_map, workspace_bytes)
+                        flashAttentionForward, forward_items, library, work_map, workspace_bytes)
 
 from . import glue  # noqa: E402  (layernorm, residual add, dX cast around the sublayer)
 from . import sublayer  # noqa: E402  (the GEMMs around the attention core)
 
 __all__ = ["glue", "sublayer", "AttentionError", "AttentionParams", "attention_backward", "attention_forward", "backward_part",
            "computeD", "flashAttentionBackward", "flashAttentionBackwardNoAlloc", "flashAttentionBackwardWorkspace",
-           "flashAttentionForward", "library",
+           "flashAttentionForward", "forward_items", "library",
            "work_map", "workspace_bytes"]

@@ -30,7 +30,7 @@ EXPORTED = ("flashAttentionForward", "computeD", "flashAttentionBackward", "meta
             "flashAttentionBackwardWorkspace", "metalllmAttnBackwardWorkspaceSize", "residualAdd",
             "layernormForward", "layernormBackward",
             "metalllmSublayerGraphCreate", "metalllmSublayerGraphLaunch", "metalllmSublayerGraphDestroy",
-            "metalllmSublayerReserve", "flashAttentionBackwardNoAlloc")
+            "metalllmSublayerReserve", "flashAttentionBackwardNoAlloc", "metalllmAttnForwardItems")
 NOALLOC_SCRATCH_BYTES = 64 << 20  # METALLLM_ATTN_NOALLOC_SCRATCH_BYTES
 
 
@@ -77,6 +77,8 @@ def _lib():
         L.metalllmAttnErrorString.restype = ctypes.c_char_p
         L.metalllmAttnWorkMap.argtypes = [ctypes.c_int, pp, ctypes.c_void_p, ctypes.c_int32]
         L.metalllmAttnWorkMap.restype = ctypes.c_int
+        L.metalllmAttnForwardItems.argtypes = [pp, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32]
+        L.metalllmAttnForwardItems.restype = ctypes.c_int
         _LIB = L
     return _LIB
 
@@ -204,6 +206,19 @@ def attention_backward(dO, q, k, v, out, lse, stream=None):
     computeD(dO, out, Dv, stream)
     flashAttentionBackward(dO, Dv, lse, q, k, v, dQ, dK, dV, stream)
     return dQ, dK, dV, Dv
+
+
+def forward_items(B: int, T: int, H: int, D: int, grid: int):
+    """(workgroup, pair, block) of every item of the persistent forward on `grid` workgroups, each
+    workgroup's items in the order it runs them."""
+    import numpy as np
+    p = AttentionParams.of(B, T, H, D)
+    n = _lib().metalllmAttnForwardItems(ctypes.byref(p), grid, None, 0)
+    _check(min(n, 0), "metalllmAttnForwardItems")
+    out = np.zeros((n, 3), dtype=np.int32)
+    _check(min(_lib().metalllmAttnForwardItems(ctypes.byref(p), grid, out.ctypes.data_as(ctypes.c_void_p), n), 0),
+           "metalllmAttnForwardItems")
+    return out
 
 
 def work_map(kind: int, B: int, T: int, H: int, D: int):

@@ -139,4 +139,25 @@ int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_
   return grid;
 }
 
+int metalllmAttnForwardItems(const AttentionParams* p, int32_t grid, int32_t* out, int32_t count) {
+  const int rc = validate(p);
+  if (rc) return rc;
+  if (grid <= 0) return METALLLM_ATTN_E_LAYOUT;
+  if (!out && count > 0) return METALLLM_ATTN_E_NULL;
+  const int npairs = (int)(p->B * p->NH);
+  const int nblk = ((int)p->M + mla::kFwdBlockM - 1) / mla::kFwdBlockM;
+  int n = 0;
+  for (int w = 0; w < grid; ++w) {
+    int pair, blk;
+    for (int k = 0; mla::fwd_item_of(w, grid, k, npairs, nblk, pair, blk); ++k, ++n) {
+      if (n < count) {
+        out[3 * n] = w;
+        out[3 * n + 1] = pair;
+        out[3 * n + 2] = blk;
+      }
+    }
+  }
+  return n;
+}
+
 }  // extern "C"

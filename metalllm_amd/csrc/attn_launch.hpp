@@ -77,7 +77,25 @@ __host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, 
   blk = last_first ? (nblk - 1 - local) : local;
 }
 
+// Item k of workgroup `bid` of a persistent grid of `grid` workgroups over npairs x nblk
+// (pair, block) items; false when the workgroup has fewer than k + 1 items. When both the pair
+// count and the grid are multiples of 8, the workgroups on XCD x (bid % 8 == x) serve the pairs
+// p = x (mod 8), so all blocks of a pair share one L2; otherwise all workgroups form one group.
+// A group's items are listed pair by pair, each pair's last (largest causal) block first, and
+// dealt in snake order over its workgroups, so each workgroup gets about the same work.
+__host__ __device__ inline bool fwd_item_of(int bid, int grid, int k, int npairs, int nblk, int& pair, int& blk) {
+  const int G = ((npairs & 7) == 0 && (grid & 7) == 0) ? 8 : 1;
+  const int x = bid % G, w = bid / G, W = grid / G;
+  const int m = k * W + ((k & 1) ? W - 1 - w : w);
+  if (m >= npairs / G * nblk) return false;
+  const int j = m / nblk, local = m - j * nblk;
+  pair = j * G + x;
+  blk = nblk - 1 - local;
+  return true;
+}
+
 constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
+constexpr int kFwdPersistT = 256;  // sequences up to this length run the persistent forward
 constexpr int kBwdBlockN = 128;  // keys owned by one dK/dV workgroup
 constexpr int kDqBlockM = 128;   // query rows owned by one dQ workgroup
 constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)

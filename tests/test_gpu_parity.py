@@ -90,6 +90,23 @@ def test_config1_slice_equals_config0(gpu):
     assert np.array_equal(out[:16], out0) and np.array_equal(lse[:16], lse0)
 
 
+@pytest.mark.parametrize("B,H,D", [(128, 6, 64), (8, 3, 128)])
+def test_persistent_forward_equals_per_item_forward(gpu, B, H, D):
+    """Sequences of T <= 256 run the persistent forward (each workgroup takes several (pair, query
+    block) items, the next item's Q rows and first K tiles loaded during the current item's last
+    step); longer ones one workgroup per item. Causal rows 0..255 of a T = 320 sequence depend
+    only on keys 0..255 and visit the same key tiles in the same order, so the T = 320 forward
+    (per item) and the T = 256 forward of the prefix (persistent; at B = 128, H = 6 two items per
+    workgroup) must agree bit for bit on those rows."""
+    print(f"case B={B} H={H} D={D}", flush=True)
+    q, k, v, _ = make_inputs(B, 320, H, D, 61)
+    out_l, lse_l = gpu_forward(q, k, v, gpu)
+    pre = lambda x: np.ascontiguousarray(x[:, :256])
+    out_s, lse_s = gpu_forward(pre(q), pre(k), pre(v), gpu)
+    assert np.array_equal(out_s, out_l[:, :256])
+    assert np.array_equal(lse_s, lse_l[:, :, :256])
+
+
 def test_config2_peaky_slice(gpu):
     """Config 2 (B=32, H=12, T=1024, D=64, Q/K x1.5): two batches checked against the oracle."""
     check_case(gpu, 32, 1024, 12, 64, 1.5, 22, b_end=2)

@@ -26,3 +26,24 @@ def test_partition(B, T, H, D, kind, blk, last_first):
     if npairs % 8 == 0:  # workgroup i runs on XCD i % 8: all blocks of a pair share one XCD
         for p in range(npairs):
             assert len(set((np.nonzero(wm[:, 0] == p)[0] % 8).tolist())) == 1
+
+
+@pytest.mark.parametrize("B,T,H,D", [(128, 256, 6, 64), (16, 256, 6, 64), (3, 192, 5, 128), (1, 64, 1, 64),
+                                     (2, 128, 3, 64)])
+@pytest.mark.parametrize("grid", [768, 512, 96, 8, 7, 1])
+def test_persistent_forward_items(B, T, H, D, grid):
+    """The persistent forward (T <= 256): every (pair, query block) item is run by exactly one
+    workgroup; when the pair count and the grid are multiples of 8, all items of a workgroup
+    belong to pairs on its XCD (workgroup w runs on XCD w % 8); each workgroup's causal work
+    (query block + 1 key tiles per item) is within one item's work of the mean."""
+    npairs, nblk = B * H, -(-T // 128)
+    items = M.forward_items(B, T, H, D, grid)
+    assert items.shape == (npairs * nblk, 3)
+    assert set(map(tuple, items[:, 1:].tolist())) == {(p, b) for p in range(npairs) for b in range(nblk)}
+    assert ((items[:, 0] >= 0) & (items[:, 0] < grid)).all()
+    if npairs % 8 == 0 and grid % 8 == 0:
+        assert (items[:, 1] % 8 == items[:, 0] % 8).all()
+    work = np.bincount(items[:, 0], weights=items[:, 2] + 1, minlength=grid)
+    used = min(grid, npairs * nblk)
+    assert work[:used].min() > 0 and (work[used:] == 0).all()
+    assert work.max() - work.sum() / used <= nblk
