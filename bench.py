@@ -101,10 +101,12 @@ def cpu_baseline(B, H, T, D, qk_scale, threads, target_s=10.0):
 
 def bench_sublayer(args):
     """one pre-LN block's attention sublayer, fwd + bwd, X bf16 [8, 2048, 768]
-    ~N(0,1), Wq/Wk/Wv/Wproj bf16 [768, 768] ~N(0, 0.02), dOut ~N(0,1), H=12 (D=64). One step = the
-    gradient zeroing of model.h:549-555, then forward computeQKV -> flashAttentionForward ->
-    projForward and backward projBackwarddW/dX -> computeD -> flashAttentionBackward ->
-    computeGradDx/Dw (model.h:446-482, 621-690). Reports ms per step and the attention share."""
+    ~N(0,1), Wq/Wk/Wv/Wproj bf16 [768, 768] ~N(0, 0.02), dOut ~N(0,1), H=12 (D=64). One step =
+    forward computeQKV -> flashAttentionForward -> projForward and backward projBackwarddW/dX ->
+    computeD -> flashAttentionBackward -> computeGradDx/Dw (model.h:446-482, 621-690), with the
+    accumulated gradients starting from zero (model.h:549-555). The per-call chain (timed per phase
+    by events) zeroes them and adds into them; the headline, the phase encoder, writes them as
+    0 + the gradient. Reports ms per step and the attention share."""
     import torch
     import metalllm_amd as M
     from metalllm_amd import sublayer as S
@@ -152,9 +154,11 @@ def bench_sublayer(args):
     attn_flop = 7.0 * B * H * T * T * D
 
     # The same step through the phase encoder: both phases enqueued by the library
-    # (metalllmSublayerEncode), then recorded once as HIP graphs and replayed. Identical work:
-    # phase 1 zeroes the same gradients and reads dOut from the sublayer's buffer; the dX cast of
-    # model.h:692 is left out (it is not part of config 4's chain).
+    # (metalllmSublayerEncode), then recorded once as HIP graphs and replayed. The same products
+    # and the same results: phase 1 writes dX and the weight gradients as 0 + the gradient (bit
+    # for bit what the per-call chain's zeroing and accumulation give) instead of zeroing them
+    # and adding into them, and reads dOut from the sublayer's buffer; the dX cast of model.h:692
+    # is left out (it is not part of config 4's chain).
     sub.dOut.copy_(dOut)
 
     def timed(fn):

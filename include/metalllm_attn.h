@@ -259,10 +259,11 @@ typedef struct metalllmSublayerGraph metalllmSublayerGraph;
 
 /* Enqueues one phase of the sublayer on `stream`, in model.h's order.
  *   phase 0 (model.h:444-483): computeQKV, flashAttentionForward, projForward.
- *   phase 1 (model.h:549-555, 620-693): zero dX, dQw, dKw, dVw, dProjw; projBackwarddW,
- *            projBackwarddX, computeD, flashAttentionBackwardWorkspace, computeGradDx,
- *            computeGradDw (one two-term split of dQ serves both), and castFloatToBfloat(dX) when
- *            dX_bf16 is set.
+ *   phase 1 (model.h:549-555, 620-693): projBackwarddW, projBackwarddX, computeD,
+ *            flashAttentionBackwardWorkspace, computeGradDx, computeGradDw, and
+ *            castFloatToBfloat(dX) when dX_bf16 is set. dX, dQw, dKw, dVw and dProjw, which
+ *            model.h zeroes before the pass and accumulates into, have one producer each here:
+ *            they are written as 0 + the gradient, bit for bit, without being zeroed or read.
  * With the block fields set: phase 0 starts with layernormForward(hidden -> X) and ends with
  * residualAdd(hidden, out -> residual); phase 1 also zeroes ln_dgamma/ln_dbeta, casts dX into
  * dStream, then runs layernormBackward(dStream) and residualAdd(dStream, dOut -> dStream).

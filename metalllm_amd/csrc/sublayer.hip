@@ -32,11 +32,11 @@
 namespace mla {  // sublayer_gemm.hip
 bool grad_dx_fused_ok(int R, int C);
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
-                          const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s);
+                          const uint16_t* Wk, const uint16_t* Wv, int R, int C, bool accumulate, hipStream_t s);
 bool grad_dw_fused_ok(int R, int C);
 size_t grad_dw_partial_floats(int R, int C);
 hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
-                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, hipStream_t s);
+                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, bool accumulate, hipStream_t s);
 }  // namespace mla
 
 namespace {
@@ -220,28 +220,30 @@ int xt_g_partials(const Ctx& c, const uint16_t* X, const uint16_t* G, int R, int
 }
 
 // dst[i] = round(dst[i] + sum_p part[p * n + i]) with the fp32 sum in p order; dst fp32 or bf16.
+// Without acc_dst the destination is written as if it held zeros (bit for bit 0 + sum), unread.
 template <bool BF16_DST>
-__global__ void __launch_bounds__(256) reduce_kernel(const float* __restrict__ part, int nparts, size_t n, void* dst) {
+__global__ void __launch_bounds__(256) reduce_kernel(const float* __restrict__ part, int nparts, size_t n, void* dst,
+                                                     bool acc_dst) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     float acc = 0.0f;
     for (int p = 0; p < nparts; ++p) acc += part[(size_t)p * n + i];
     if (BF16_DST) {
       uint16_t* d = (uint16_t*)dst;
-      d[i] = rne_bf16(__uint_as_float((uint32_t)d[i] << 16) + acc);
+      d[i] = rne_bf16((acc_dst ? __uint_as_float((uint32_t)d[i] << 16) : 0.0f) + acc);
     } else {
       float* d = (float*)dst;
-      d[i] = d[i] + acc;
+      d[i] = (acc_dst ? d[i] : 0.0f) + acc;
     }
   }
 }
 
-int reduce_into(const Ctx& c, const float* part, int nparts, size_t n, void* dst, bool bf16_dst) {
+int reduce_into(const Ctx& c, const float* part, int nparts, size_t n, void* dst, bool bf16_dst, bool accumulate = true) {
   if (c.query) return METALLLM_ATTN_OK;
   const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
   if (bf16_dst)
-    hipLaunchKernelGGL(reduce_kernel<true>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst);
+    hipLaunchKernelGGL(reduce_kernel<true>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst, accumulate);
   else
-    hipLaunchKernelGGL(reduce_kernel<false>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst);
+    hipLaunchKernelGGL(reduce_kernel<false>, dim3(blocks), dim3(256), 0, c.stream, part, nparts, n, dst, accumulate);
   return hipGetLastError() == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 
@@ -273,12 +275,13 @@ int op_proj_fwd(const Ctx& c, const uint16_t* attn_out, const uint16_t* proj_w, 
   return gemm_rm(c, false, false, R, C, C, attn_out, BF, C, proj_w, BF, C, 0.0f, out, BF, C);
 }
 
-// partial: at least row_chunks(R) * C * C floats
+// partial: at least row_chunks(R) * C * C floats. accumulate = false: dProjw is written as if it
+// held zeros (the phase encoder; every op_* below takes the same flag).
 int op_proj_dw(const Ctx& c, const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, int R, int C,
-               float* partial) {
+               float* partial, bool accumulate = true) {
   const int parts = row_chunks(R);
   TRY(xt_g_partials(c, attn_out, dZ, R, C, parts, partial));
-  return reduce_into(c, partial, parts, (size_t)C * C, dProjw, true);
+  return reduce_into(c, partial, parts, (size_t)C * C, dProjw, true, accumulate);
 }
 
 int op_proj_dx(const Ctx& c, const uint16_t* dZ, const uint16_t* proj_w, uint16_t* dAttn, int R, int C) {
@@ -289,13 +292,15 @@ int op_proj_dx(const Ctx& c, const uint16_t* dZ, const uint16_t* proj_w, uint16_
 // which reads the fp32 dQ itself; other shapes use the library on hi, lo, the two-term bf16 split
 // of dQ (split_dq).
 int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, const uint16_t* vw, const float* dQ,
-               const uint16_t* hi, const uint16_t* lo, const uint16_t* dK, const uint16_t* dV, int R, int C) {
+               const uint16_t* hi, const uint16_t* lo, const uint16_t* dK, const uint16_t* dV, int R, int C,
+               bool accumulate = true) {
   if (mla::grad_dx_fused_ok(R, C)) {
     if (c.query) return METALLLM_ATTN_OK;
-    return mla::launch_grad_dx(dX, dQ, dK, dV, qw, kw, vw, R, C, c.stream) == hipSuccess ? METALLLM_ATTN_OK
-                                                                                        : METALLLM_ATTN_E_LAUNCH;
+    return mla::launch_grad_dx(dX, dQ, dK, dV, qw, kw, vw, R, C, accumulate, c.stream) == hipSuccess
+               ? METALLLM_ATTN_OK
+               : METALLLM_ATTN_E_LAUNCH;
   }
-  TRY(gemm_rm(c, false, true, R, C, C, hi, BF, C, qw, BF, C, 1.0f, dX, F32, C));
+  TRY(gemm_rm(c, false, true, R, C, C, hi, BF, C, qw, BF, C, accumulate ? 1.0f : 0.0f, dX, F32, C));
   TRY(gemm_rm(c, false, true, R, C, C, lo, BF, C, qw, BF, C, 1.0f, dX, F32, C));
   TRY(gemm_rm(c, false, true, R, C, C, dK, BF, C, kw, BF, C, 1.0f, dX, F32, C));
   return gemm_rm(c, false, true, R, C, C, dV, BF, C, vw, BF, C, 1.0f, dX, F32, C);
@@ -306,10 +311,10 @@ int op_grad_dx(const Ctx& c, float* dX, const uint16_t* qw, const uint16_t* kw, 
 // other shapes use the library on hi, lo, the two-term bf16 split of dQ (split_dq).
 int op_grad_dw(const Ctx& c, const uint16_t* x, const float* dQ, const uint16_t* hi, const uint16_t* lo,
                const uint16_t* dK, const uint16_t* dV, float* dQw, uint16_t* dKw, uint16_t* dVw, int R, int C,
-               float* part) {
+               float* part, bool accumulate = true) {
   if (mla::grad_dw_fused_ok(R, C)) {
     if (c.query) return METALLLM_ATTN_OK;
-    return mla::launch_grad_dw(x, dQ, dK, dV, dQw, dKw, dVw, part, R, C, c.stream) == hipSuccess
+    return mla::launch_grad_dw(x, dQ, dK, dV, dQw, dKw, dVw, part, R, C, accumulate, c.stream) == hipSuccess
                ? METALLLM_ATTN_OK
                : METALLLM_ATTN_E_LAUNCH;
   }
@@ -318,11 +323,11 @@ int op_grad_dw(const Ctx& c, const uint16_t* x, const float* dQ, const uint16_t*
   // dQw: the partials of X^T.hi and X^T.lo together, added into dQw once
   TRY(xt_g_partials(c, x, hi, R, C, parts, part));
   TRY(xt_g_partials(c, x, lo, R, C, parts, part + parts * cc));
-  TRY(reduce_into(c, part, 2 * parts, cc, dQw, false));
+  TRY(reduce_into(c, part, 2 * parts, cc, dQw, false, accumulate));
   TRY(xt_g_partials(c, x, dK, R, C, parts, part));
-  TRY(reduce_into(c, part, parts, cc, dKw, true));
+  TRY(reduce_into(c, part, parts, cc, dKw, true, accumulate));
   TRY(xt_g_partials(c, x, dV, R, C, parts, part));
-  return reduce_into(c, part, parts, cc, dVw, true);
+  return reduce_into(c, part, parts, cc, dVw, true, accumulate);
 }
 
 // Zeroes up to 8 buffers in one launch (a fill kernel: no memset node when captured into a
@@ -501,16 +506,14 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
     if (block && !c.query) TRY(residualAdd(b->hidden, b->out, b->residual, (uint32_t)e, s));  // model.h:483
     return METALLLM_ATTN_OK;
   }
-  // model.h:549-555 zeroes the accumulated gradients before the pass (the attention backward
-  // writes dQ, dK and dV in full), and for the block model.h:545-546 the layernorm's; one launch
-  const std::pair<void*, size_t> grads[] = {{b->dX, e * 4}, {b->dQw, (size_t)C * C * 4}, {b->dKw, (size_t)C * C * 2},
-                                            {b->dVw, (size_t)C * C * 2}, {b->dProjw, (size_t)C * C * 2}};
-  if (block)
-    TRY(zero_buffers(c, {grads[0], grads[1], grads[2], grads[3], grads[4], {b->ln_dgamma, (size_t)C * 4},
-                         {b->ln_dbeta, (size_t)C * 4}}));
-  else
-    TRY(zero_buffers(c, {grads[0], grads[1], grads[2], grads[3], grads[4]}));
-  TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial));
+  // model.h:549-555 zeroes the accumulated gradients before the pass and the kernels add into
+  // them. Each of dX, dQw, dKw, dVw and dProjw has a single producer in this phase, so the phase
+  // runs them in write mode instead: the result is bit for bit 0 + the gradient (-0 becomes +0),
+  // without the zeroing pass and without reading the destinations. The attention backward writes
+  // dQ, dK and dV in full; the block's layernorm gradients (model.h:545-546), which its backward
+  // adds into with atomics, are zeroed here.
+  if (block) TRY(zero_buffers(c, {{b->ln_dgamma, (size_t)C * 4}, {b->ln_dbeta, (size_t)C * 4}}));
+  TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial, false));
   TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
   if (!c.query) {
     TRY(computeD(b->dAttn, b->attn_out, b->Dsum, p, s));
@@ -524,8 +527,8 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   } else {
     split = nullptr;
   }
-  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C));
-  TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial));
+  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
+  TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial, false));
   if (c.query) return METALLLM_ATTN_OK;
   if (block) {  // model.h:692-695
     TRY(castFloatToBfloat(b->dX, b->dStream, (uint32_t)e, s));

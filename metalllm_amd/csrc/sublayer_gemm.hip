@@ -42,6 +42,9 @@ __device__ __forceinline__ u32x4 lds_ld16(uint32_t a) { return *(const __attribu
 __device__ __forceinline__ void lds_st16(uint32_t a, u32x4 v) { *(__attribute__((address_space(3))) u32x4*)(uintptr_t)a = v; }
 __device__ __forceinline__ void lds_st8(uint32_t a, u32x2 v) { *(__attribute__((address_space(3))) u32x2*)(uintptr_t)a = v; }
 
+// ACC: dX += the products (the reference's contract); otherwise dX = 0 + the products, written
+// without reading dX (the phase encoder, which would zero dX just before).
+template <bool ACC>
 __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
                                                         const uint16_t* __restrict__ Wq, const uint16_t* __restrict__ Wk,
@@ -192,7 +195,10 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
       for (int g = 0; g < 4; ++g) {
         f32x4* p = (f32x4*)(row + 32 * mi + 8 * g);
         const f32x4 v = f32x4{acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2], acc[mi][ni][4 * g + 3]};
-        *p = *p + v;
+        if (ACC)
+          *p = *p + v;
+        else
+          *p = v + 0.0f;  // bit for bit 0 + v (-0 becomes +0)
       }
   }
 }
@@ -388,10 +394,11 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
 }
 
 // dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw = bf16(previous + the sum of
-// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread.
+// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread. Without
+// acc the destinations are written as if they held zeros (bit for bit 0 + sum), and not read.
 __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __restrict__ part, float* __restrict__ dQw,
                                                                uint16_t* __restrict__ dKw, uint16_t* __restrict__ dVw,
-                                                               int C, int nq, int nkv) {
+                                                               int C, int nq, int nkv, bool acc_dst) {
   const size_t cc = (size_t)C * C, n4 = cc / 4;
   for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < 3 * n4; e += (size_t)gridDim.x * blockDim.x) {
     const int w = (int)(e / n4);
@@ -401,10 +408,10 @@ __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __rest
     for (int p = 1; p < np; ++p) acc += *(const f32x4*)(part + (size_t)(p0 + p) * cc + o);
     if (w == 0) {
       f32x4* d = (f32x4*)(dQw + o);
-      *d = *d + acc;
+      *d = (acc_dst ? *d : f32x4{0.0f, 0.0f, 0.0f, 0.0f}) + acc;
     } else {
       u32x2* d = (u32x2*)((w == 1 ? dKw : dVw) + o);
-      const u32x2 old = *d;
+      const u32x2 old = acc_dst ? *d : u32x2{0u, 0u};
       *d = u32x2{pack_bf16(bf_lo(old[0]) + acc[0], bf_hi(old[0]) + acc[1]),
                  pack_bf16(bf_lo(old[1]) + acc[2], bf_hi(old[1]) + acc[3])};
     }
@@ -447,21 +454,24 @@ size_t grad_dw_partial_floats(int R, int C) {
 }
 
 hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
-                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, hipStream_t s) {
+                          uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, bool accumulate, hipStream_t s) {
   const GwShape sh = grad_dw_shape(R, C, device_cus());
   hipLaunchKernelGGL(grad_dw_kernel, dim3((unsigned)sh.items), dim3(256), 0, s, X, dQ, dK, dV, partial, sh);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n4 = 3 * (size_t)C * C / 4;
   hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
-                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv);
+                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv, accumulate);
   return hipGetLastError();
 }
 
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
-                          const uint16_t* Wk, const uint16_t* Wv, int R, int C, hipStream_t s) {
+                          const uint16_t* Wk, const uint16_t* Wv, int R, int C, bool accumulate, hipStream_t s) {
   const int items = (R / kGxTile) * (C / kGxTile);
-  hipLaunchKernelGGL(grad_dx_kernel, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
+  if (accumulate)
+    hipLaunchKernelGGL(grad_dx_kernel<true>, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
+  else
+    hipLaunchKernelGGL(grad_dx_kernel<false>, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
   return hipGetLastError();
 }
 
