@@ -480,6 +480,13 @@ int fwd_resident() {
   return r;
 }
 
+// Fills the resident-workgroup caches of the current device (callers about to capture a stream
+// into a graph prime them first, so that no device query runs during the capture).
+void forward_prepare() {
+  (void)fwd_resident<64>();
+  (void)fwd_resident<128>();
+}
+
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s) {
   const int nqb = (a.T + kFwdBlockM - 1) / kFwdBlockM;
   const int items = a.B * a.H * nqb;

@@ -49,6 +49,7 @@ inline size_t ds_scratch_bytes(int B, int H, int T) {
 }
 
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s);
+void forward_prepare();  // device queries of launch_forward, done ahead of a stream capture
 hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
 hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);     // dK, dV (key-owner)
 hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s);  // dQ (query-owner)

@@ -29,6 +29,10 @@
 
 #include "../../include/metalllm_attn.h"
 
+namespace mla {  // attn_fwd.hip
+void forward_prepare();
+}  // namespace mla
+
 namespace mla {  // sublayer_gemm.hip
 bool grad_dx_fused_ok(int R, int C);
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
@@ -567,6 +571,7 @@ int build_graph(metalllmSublayerGraph* g, const metalllmSublayerBuffers* b, cons
     return METALLLM_ATTN_E_LIBRARY;
   }
   if (rocblas_set_workspace(g->h, g->workspace, ws) != rocblas_status_success) return METALLLM_ATTN_E_LIBRARY;
+  mla::forward_prepare();  // the forward's device queries, before the capture
   hipStream_t cap = nullptr;
   if (hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return METALLLM_ATTN_E_LIBRARY;
   int rc = rocblas_set_stream(g->h, cap) == rocblas_status_success ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LIBRARY;
