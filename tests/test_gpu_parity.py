@@ -81,6 +81,26 @@ def test_forward_backward_parity(gpu, B, T, H, D, s, seed):
     check_case(gpu, B, T, H, D, s, seed)
 
 
+def _sweep_cases(n=14, seed=2024):
+    """Seeded shape sweep: T every multiple of 64 up to 640 (short fused backward and persistent
+    forward at T <= 256, both dQ rings above), odd and even head and batch counts (pair counts
+    that are and are not multiples of 8), both head sizes and both Q/K scales."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = (64, 128)[i % 2]
+        T = 64 * int(rng.integers(1, 11))
+        B = int(rng.integers(1, 4))
+        H = int(rng.integers(1, 9 if T <= 256 else 5))
+        cases.append((B, T, H, D, (1.0, 1.5)[int(rng.integers(0, 2))], 100 + i))
+    return cases
+
+
+@pytest.mark.parametrize("B,T,H,D,s,seed", _sweep_cases())
+def test_shape_sweep(gpu, B, T, H, D, s, seed):
+    check_case(gpu, B, T, H, D, s, seed)
+
+
 def test_config1_slice_equals_config0(gpu):
     """Config 1 (B=128) on the GPU; its first 16 batches are config 0's inputs bit for bit, and are
     checked against the oracle."""
