@@ -263,24 +263,25 @@ def main():
     # flashAttentionBackward == part 0 then part 1. The bench launches the parts itself so that
     # each kernel is timed by its own events. The workspace path writes dQ in full; the
     # recomputing path adds into dQ (the reference's contract), so its steps zero dQ first.
+    # ev: None (untimed), 5 events (a marker before, between and after the kernels: the phase
+    # spans) or 2 events (start and end only: the headline step span, free of the markers'
+    # own cost, which is a few microseconds each)
     def step(ev=None, parts=(2, 3)):
         flush.fill_(parts[0])
+        mark = (lambda i: ev[i].record(stream)) if ev is not None and len(ev) == 5 else (lambda i: None)
         if ev is not None:
             ev[0].record(stream)
         M.flashAttentionForward(q, k, v, out, lse, stream, p)
-        if ev is not None:
-            ev[1].record(stream)
+        mark(1)
         M.computeD(dO, out, Dv, stream, p)
-        if ev is not None:
-            ev[2].record(stream)
+        mark(2)
         if parts[0] == 0:
             dQ.zero_()  # the memset the reference's caller does (model.h:549), timed with the backward
         M.backward_part(parts[0], dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p, workspace=ws)
-        if ev is not None:
-            ev[3].record(stream)
+        mark(3)
         M.backward_part(parts[1], dO, Dv, lse, q, k, v, dQ, dK, dV, stream, p, workspace=ws)
         if ev is not None:
-            ev[4].record(stream)
+            ev[-1].record(stream)
 
     # the recomputing backward, for comparison (its own warmup and events)
     for _ in range(2):
@@ -294,11 +295,17 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    # phase spans: steps with markers between the kernels
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    # headline: the same steps with one event pair each
+    plain = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(events[i])
+        step(plain[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
@@ -316,9 +323,11 @@ def main():
     med = lambda xs: xs[len(xs) // 2]
     ff, fb = flops(B, H, T, D)
     unit = B * H * T * T * D  # one causal T x T x D product over all (b, h)
-    # headline: the median over the timed steps of each step's event span (first kernel to last);
-    # the wall-clock mean (which also covers the cache flush between steps) is reported beside it
-    ms_per_step = med(span(0, 4))
+    # headline: the median over the timed steps of each step's event span (one pair around the
+    # kernels); the wall-clock mean of those steps (which also covers the cache flush between
+    # steps) is reported beside it, and so is the span of the marked steps
+    ms_per_step = med(span(0, 1, plain))
+    marked_ms = med(span(0, 4))
     wall_ms = wall * 1e3 / args.steps
     value = (ff + fb) / (ms_per_step * 1e-3) / 1e12
     # dominant kernel: the dK/dV kernel (4 products: S, dP, dV = P^T dO, dK = dS^T Q)
@@ -393,8 +402,11 @@ def main():
         "config": {"workload": f"config{args.config}: causal attention fwd+computeD+bwd, {desc}",
                    "B": B, "H": H, "T": T, "D": D, "qk_scale": qk_scale, "causal": True},
         "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
-        "timing": "median of per-step HIP event spans; 512 MB written between steps (L2 and Infinity Cache flush)",
+        "timing": "median of per-step HIP event spans (one event pair around fwd, computeD and bwd); "
+                  "512 MB written between steps (L2 and Infinity Cache flush); phases from as many steps "
+                  "again with a marker between the kernels",
         "wall_ms_per_step_incl_flush": round(wall_ms, 4),
+        "marked_ms_per_step": round(marked_ms, 4),
         "phases": {
             "fwd_ms_median": round(med(fwd_ms), 4), "computeD_ms_median": round(med(cd_ms), 4),
             "bwd_ms_median": round(med(bwd_ms), 4), "bwd_dkdv_ms_median": round(med(kv_ms), 4),

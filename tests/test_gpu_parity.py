@@ -110,21 +110,22 @@ def test_config1_slice_equals_config0(gpu):
     assert np.array_equal(out[:16], out0) and np.array_equal(lse[:16], lse0)
 
 
-@pytest.mark.parametrize("B,H,D", [(128, 6, 64), (8, 3, 128)])
-def test_persistent_forward_equals_per_item_forward(gpu, B, H, D):
+@pytest.mark.parametrize("B,H,D,Tp", [(128, 6, 64, 256), (100, 3, 64, 192), (97, 3, 64, 64), (8, 3, 128, 256)])
+def test_persistent_forward_equals_per_item_forward(gpu, B, H, D, Tp):
     """Sequences of T <= 256 run the persistent forward (each workgroup takes several (pair, query
     block) items, the next item's Q rows and first K tiles loaded during the current item's last
-    step); longer ones one workgroup per item. Causal rows 0..255 of a T = 320 sequence depend
-    only on keys 0..255 and visit the same key tiles in the same order, so the T = 320 forward
-    (per item) and the T = 256 forward of the prefix (persistent; at B = 128, H = 6 two items per
-    workgroup) must agree bit for bit on those rows."""
-    print(f"case B={B} H={H} D={D}", flush=True)
+    step); longer ones one workgroup per item. Causal rows 0..Tp-1 of a T = 320 sequence depend
+    only on keys 0..Tp-1 and visit the same key tiles in the same order, so the T = 320 forward
+    (per item) and the T = Tp forward of the prefix (persistent) must agree bit for bit on those
+    rows. At B = 128, H = 6 each workgroup takes two items; 300 and 291 pairs are not multiples
+    of 8 (one group of workgroups), and at Tp = 64 an item has one key tile."""
+    print(f"case B={B} H={H} D={D} Tp={Tp}", flush=True)
     q, k, v, _ = make_inputs(B, 320, H, D, 61)
     out_l, lse_l = gpu_forward(q, k, v, gpu)
-    pre = lambda x: np.ascontiguousarray(x[:, :256])
+    pre = lambda x: np.ascontiguousarray(x[:, :Tp])
     out_s, lse_s = gpu_forward(pre(q), pre(k), pre(v), gpu)
-    assert np.array_equal(out_s, out_l[:, :256])
-    assert np.array_equal(lse_s, lse_l[:, :, :256])
+    assert np.array_equal(out_s, out_l[:, :Tp])
+    assert np.array_equal(lse_s, lse_l[:, :, :Tp])
 
 
 def test_config2_peaky_slice(gpu):
