@@ -12,7 +12,8 @@
 // trip and without a separate split pass through HBM.
 //
 // computeGradDx: all three products accumulate into one set of fp32 accumulators, so dX is read
-// and written once instead of once per product. Tiling: a workgroup of 4 waves computes a 128 (rows r) x 128 (features i) tile of dX as
+// and written once instead of once per product. Tiling: a workgroup of 4 waves computes a 128
+// (rows r) x 128 (features i) tile of dX as
 // dX^T = W . G^T (m = i, n = r, k = j): the A operand is a weight row W[i][j..j+7] and the B
 // operand a gradient row G[r][j..j+7], both 16-byte reads from row-major LDS tiles (pitch 72
 // elements: conflict-free 16-byte row reads), and each lane ends with four consecutive i of one
