@@ -128,6 +128,32 @@ def test_persistent_forward_equals_per_item_forward(gpu, B, H, D, Tp):
     assert np.array_equal(lse_s, lse_l[:, :, :Tp])
 
 
+ORACLE_FIXTURES = sorted(n[len("oracle_"):-len(".npz")] for n in os.listdir(os.path.join(HERE, "golden"))
+                         if n.startswith("oracle_") and n.endswith(".npz"))
+
+
+@pytest.mark.parametrize("name", ORACLE_FIXTURES)
+def test_committed_fixtures(gpu, name):
+    """The GPU path on the committed inputs of tests/golden/oracle_<name>.npz against the committed
+    oracle outputs (B=1, H=2, T=128, D 64 or 128, normal or peaky): LSE within 1e-3, O within
+    max(1e-2, one bf16 spacing), computeD on the stored dO and O bit for bit, and both backward
+    entry points on the stored D and LSE within 2e-2 of max |grad|."""
+    print(f"fixture {name}", flush=True)
+    d = np.load(os.path.join(HERE, "golden", f"oracle_{name}.npz"))
+    q, k, v, g = d["q"], d["k"], d["v"], d["dO"]
+    out, lse = gpu_forward(q, k, v, gpu)
+    assert float(np.abs(lse - d["lse"]).max()) <= 1e-3
+    _, beyond, _ = out_error(out, d["out"])
+    assert beyond == 0
+    assert np.array_equal(gpu_compute_d(g, d["out"], gpu), d["D"])
+    for ws in (False, True):
+        dQ, dK, dV = gpu_backward(g, d["D"], d["lse"], q, k, v, gpu, workspace=ws)
+        for n, x in (("dQ", dQ), ("dK", dK), ("dV", dV)):
+            e = rel_to_max(x, d[n])
+            print(f"  {n}{' (workspace)' if ws else ''}: rel-to-max {e:.3g}")
+            assert e <= 2e-2, n
+
+
 def test_config2_peaky_slice(gpu):
     """Config 2 (B=32, H=12, T=1024, D=64, Q/K x1.5): two batches checked against the oracle."""
     check_case(gpu, 32, 1024, 12, 64, 1.5, 22, b_end=2)

@@ -175,6 +175,27 @@ def test_batch_slice_is_independent():
     assert np.array_equal(O.normal_bf16((3, 64, 2, 64), 9, O.TID_Q)[:1], O.normal_bf16((1, 64, 2, 64), 9, O.TID_Q))
 
 
+ORACLE_FIXTURES = sorted(n[len("oracle_"):-len(".npz")] for n in os.listdir(os.path.join(HERE, "golden"))
+                         if n.startswith("oracle_") and n.endswith(".npz"))
+
+
+@pytest.mark.parametrize("name", ORACLE_FIXTURES)
+@pytest.mark.parametrize("threads", [1, 4])
+def test_oracle_regression_fixtures(name, threads):
+    """tests/golden/oracle_<name>.npz (written by tests/golden/make_oracle_fixtures.py): the input
+    generator must reproduce the stored Q, K, V, dO from the stored seed, and the oracle must
+    reproduce the stored O, LSE, D, dQ, dK, dV bit for bit, on any thread count."""
+    from tests.attn_case import make_inputs, oracle_all
+    d = np.load(os.path.join(HERE, "golden", f"oracle_{name}.npz"))
+    B, T, H, D = d["q"].shape
+    q, k, v, g = make_inputs(B, T, H, D, int(d["seed"]), float(d["qk_scale"]))
+    for n, x in (("q", q), ("k", k), ("v", v), ("dO", g)):
+        assert np.array_equal(x, d[n]), n
+    r = oracle_all(q, k, v, g, threads=threads)
+    for n in ("out", "lse", "D", "dQ", "dK", "dV"):
+        assert np.array_equal(r[n], d[n]), n
+
+
 def test_mfma_model_matches_recorded_hardware():
     cases = json.load(open(os.path.join(HERE, "golden", "mfma_rounding_cases.json")))["cases"]
     assert len(cases) >= 70
