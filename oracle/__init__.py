@@ -68,8 +68,8 @@ def params(B: int, T: int, H: int, D: int) -> AttentionParams:
 
 def opts(threads: int = 0, b_begin: int = 0, b_end: int = 0, gemm_model: int = GEMM_MFMA,
          bwd_mode: int = BWD_REFERENCE, d_round: int = 1, fwd_lazy: float = 0.0) -> OracleOpts:
-    """fwd_lazy > 0 is a diagnosis mode (the GPU forward's lazy softmax reference point); 0 is the
-    reference's exact running max."""
+    """fwd_lazy > 0 is a diagnosis mode (a lazy softmax reference point that moves only by more
+    than fwd_lazy log2 units); 0 is the reference's exact running max, which the GPU forward uses."""
     return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round, fwd_lazy)
 
 

@@ -77,8 +77,9 @@ typedef struct {
   int d_round;      // 1: D rounded to bf16 (the reference stores bf16 D); 0: fp32 D
   float fwd_lazy;   // 0: the reference's running max (moves to every larger tile max, :127-134).
                     // t > 0: a diagnosis mode that moves the softmax reference point only when the
-                    // tile max exceeds it by more than t in log2 units, as the GPU forward does
-                    // (t = 8); P = bf16(exp(s - m)) is then rounded relative to that point
+                    // tile max exceeds it by more than t in log2 units (a lazy scheme a forward
+                    // may use to skip O rescales); P = bf16(exp(s - m)) is then rounded relative
+                    // to that point, away from the reference's rounding point
 } OracleOpts;
 
 }  // extern "C"

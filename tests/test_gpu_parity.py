@@ -17,8 +17,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from tests.attn_case import (f32, gpu_backward, gpu_compute_d, gpu_forward, make_inputs, out_error, out_exceptions,
-                             rel_to_max, to_gpu, to_np)
+from tests.attn_case import (bf16_ulp, f32, gpu_backward, gpu_compute_d, gpu_forward, make_inputs, out_error,
+                             out_exceptions, rel_to_max, to_gpu, to_np)
 from tests.lse_flips import diagnose_row, rows_beyond
 
 pytestmark = pytest.mark.gpu
@@ -291,6 +291,34 @@ def test_causal_mask_with_one_hot_v(gpu, B, T, H, D):
     r_out, r_lse = O.forward(q, k, v)
     assert np.abs(lse - r_lse).max() <= 1e-3
     assert np.abs(A - f32(r_out)).max() <= 1e-2
+
+
+@pytest.mark.parametrize("D,s,seed", [(64, 3.0, 71), (128, 3.0, 72), (64, 5.0, 73)])
+def test_sharp_attention(gpu, D, s, seed):
+    """Q and K scaled by 3 and 5 (score standard deviations of about 9 and 25 against 1 for
+    unscaled inputs): the running max moves by far more than the rescale threshold within a row,
+    so the O rescale runs with factors far below 1, and most rows put nearly all their weight on
+    one key. Forward, computeD and both backward entry points against the oracle at the usual
+    bars."""
+    check_case(gpu, 1, 512, 2, D, s, seed)
+
+
+@pytest.mark.parametrize("T,D", [(320, 64), (192, 128)])
+def test_uniform_scores_closed_form(gpu, T, D):
+    """Q = 0 makes every score 0, so row i attends uniformly to keys 0..i (attention.metal:111-158
+    with S = 0): LSE_i = log(i + 1) (the running max is 0 and the row sum counts exact ones) and
+    O_i = mean of V_0..V_i, rounded once to bf16 after an fp32 sum."""
+    B, H = 1, 2
+    print(f"case T={T} D={D}", flush=True)
+    _, k, v, _ = make_inputs(B, T, H, D, 81)
+    q = np.zeros_like(k)
+    out, lse = gpu_forward(q, k, v, gpu)
+    ref_lse = np.log(np.arange(1, T + 1, dtype=np.float64))
+    assert np.abs(lse.astype(np.float64) - ref_lse[None, None, :]).max() <= 2e-6
+    V = f32(v).astype(np.float64)
+    mean = np.cumsum(V, axis=1) / np.arange(1, T + 1, dtype=np.float64)[None, :, None, None]
+    err = np.abs(f32(out).astype(np.float64) - mean)
+    assert (err <= bf16_ulp(mean.astype(np.float32)).astype(np.float64) + 1e-7).all(), float(err.max())
 
 
 def test_config2_against_plain_fp32_order(gpu):
