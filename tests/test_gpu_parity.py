@@ -164,6 +164,33 @@ def test_config3_slice(gpu):
     check_case(gpu, 1, 4096, 16, 128, 1.0, 23)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_long_sequence_extends_shorter(gpu, D):
+    """T = 8192 (twice config 3's length) against T = 4096 on the same leading rows, both entry
+    points of the backward. Causal rows 0..4095 of the forward depend only on keys 0..4095 and
+    visit the same tiles in the same order, so O and LSE agree bit for bit; with dO zero on rows
+    4096.., those rows have D = 0, dP = 0 and dS = 0, so they add exact zeros to every gradient:
+    dQ of rows 0..4095 and dK, dV of keys 0..4095 agree bit for bit with the T = 4096 backward,
+    and the rest is zero. The T = 4096 path is checked against the oracle at config 3."""
+    B, H, T, Ts = 1, 2, 8192, 4096
+    print(f"case T={T} vs {Ts} H={H} D={D}", flush=True)
+    q, k, v, g = make_inputs(B, T, H, D, 95)
+    g[:, Ts:] = 0
+    pre = lambda x: np.ascontiguousarray(x[:, :Ts])
+    out_l, lse_l = gpu_forward(q, k, v, gpu)
+    out_s, lse_s = gpu_forward(pre(q), pre(k), pre(v), gpu)
+    assert np.array_equal(out_s, out_l[:, :Ts]) and np.array_equal(lse_s, lse_l[:, :, :Ts])
+    D_l = gpu_compute_d(g, out_l, gpu)
+    D_s = gpu_compute_d(pre(g), out_s, gpu)
+    assert np.array_equal(D_s, D_l[:, :, :Ts]) and not D_l[:, :, Ts:].any()
+    for ws in (False, True):
+        dQ_l, dK_l, dV_l = gpu_backward(g, D_l, lse_l, q, k, v, gpu, workspace=ws)
+        dQ_s, dK_s, dV_s = gpu_backward(pre(g), D_s, lse_s, pre(q), pre(k), pre(v), gpu, workspace=ws)
+        for n, long_, short in (("dQ", dQ_l, dQ_s), ("dK", dK_l, dK_s), ("dV", dV_l, dV_s)):
+            assert np.array_equal(long_[:, :Ts], short), n
+            assert not f32(long_[:, Ts:]).any(), n
+
+
 def test_config3_full_size_properties(gpu):
     """Config 3 at full size: row 0 of every head equals V row 0 bit for bit (causal index logic),
     LSE finite, forward and backward deterministic across runs, sum over keys of dV equal to the
