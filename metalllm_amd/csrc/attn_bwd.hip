@@ -103,23 +103,29 @@ struct LdsDsSink {
 };
 
 // The per-wave part of the key-owner backward: 32 keys of one (b,h), their K and V rows as
-// matrix-core B operands, their dK/dV state (bf16 pairs) and the query-tile step over a query
-// tile staged in LDS (a "stage": Q tile, dO tile, then lse*log2(e) and D of its 64 rows, in the
-// BwdCfg layout). Used by bwd_kernel (streamed query tiles) and bwd_short_kernel (all query
-// tiles of a short sequence resident).
-template <int D>
+// matrix-core B operands, their dK/dV state and the query-tile step over a query tile staged in
+// LDS (a "stage": Q tile, dO tile, then lse*log2(e) and D of its 64 rows, in the BwdCfg layout).
+// Used by bwd_kernel (streamed query tiles) and bwd_short_kernel (all query tiles of a short
+// sequence resident). F32S_ (D = 64 only) holds the state as fp32 (see below).
+template <int D, bool F32S_ = false>
 struct DkdvWave {
   using C = BwdCfg<D>;
+  static_assert(!F32S_ || D == 64, "the fp32 state fits the register budget at D = 64 only");
   int h, key;
   float scale, sl;
   uint32_t row_rd, tr_rd, st_rd;
   u32x4 Kr[C::KC], Vr[C::KC];
-  // dK^T, dV^T (m = d, n = key) as packed bf16 pairs of accumulator rows (r, r+1)
-  uint32_t dKp[C::DT][8], dVp[C::DT][8];
-  // Update accumulators: chain n (dV of d tile n for n < DT, else dK of d tile n - DT) runs in
-  // block n % 2; while it runs, the other block's previous chain is rounded back into the bf16
-  // state and the next chain's state is widened into it.
+  // dK^T, dV^T (m = d, n = key), chain n = dV of d tile n for n < DT, else dK of d tile n - DT.
+  // Packed: bf16 pairs of accumulator rows (r, r+1); chain n runs in update block n % 2, and
+  // while it runs the other block's previous chain is rounded back into the bf16 state and the
+  // next chain's state is widened into it. F32S: the state is held as fp32 values that are
+  // bf16-exact (at D = 64 as many registers as the packed state plus the two blocks), each
+  // chain's products accumulate into it directly and it is rounded in place after every query
+  // tile, one instruction per value instead of a widening and a packing; bit-identical results.
+  static constexpr bool F32S = F32S_;
+  uint32_t dKp[F32S ? 1 : C::DT][8], dVp[F32S ? 1 : C::DT][8];
   f32x16 acc[2];
+  f32x16 st32[F32S ? 2 * C::DT : 1];
   // dS of the latest query tile, packed bf16 (index 8t + r/2); stored by the sink in the first
   // slots of the next tile (or after the last one)
   uint32_t dS[16];
@@ -135,15 +141,20 @@ struct DkdvWave {
     // of a 32-d tile; source lane s = lane%16 points at query row 4h + s/4 (+8 for the second read)
     tr_rd = 2 * ((4 * h + (s16 >> 2)) * C::P + 16 * (g16 & 1) + 4 * (s16 & 3));
     st_rd = 4 * (4 * h);  // statistics of query row 32t + 8g + 4h + i at +4(32t + 8g + i)
+    if constexpr (F32S) {
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
+      for (int n = 0; n < 2 * C::DT; ++n) st32[n] = zero16();
+    } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        dKp[dt][i] = 0u;
-        dVp[dt][i] = 0u;
-      }
-    acc[0] = zero16();
-    acc[1] = zero16();
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dKp[dt][i] = 0u;
+          dVp[dt][i] = 0u;
+        }
+      acc[0] = zero16();
+      acc[1] = zero16();
+    }
   }
   // own K and V rows: lane holds row `key_ld`, d = 16c + 8h .. +7
   __device__ __forceinline__ void load_rows(const uint16_t* Kg, const uint16_t* Vg, int key_ld, int rs) {
@@ -171,8 +182,23 @@ struct DkdvWave {
       acc[n & 1][2 * u + 1] = hi;
     }
   }
+  // F32S: values r0 .. r1-1 of chain n rounded in place to bf16
+  __device__ __forceinline__ void round_chain(int n, int r0, int r1) {
+#pragma unroll
+    for (int r = r0; r < r1; r += 2) {
+      float a = round_bf16(st32[n][r]), b = round_bf16(st32[n][r + 1]);
+      pin(a, b);
+      st32[n][r] = a;
+      st32[n][r + 1] = b;
+    }
+  }
   // the last chain of the last query tile back into the state
-  __device__ __forceinline__ void finish() { pack_pairs(2 * C::DT - 1, 0, 8); }
+  __device__ __forceinline__ void finish() {
+    if constexpr (F32S)
+      round_chain(2 * C::DT - 1, 0, 16);
+    else
+      pack_pairs(2 * C::DT - 1, 0, 8);
+  }
   // dK, dV rows of this lane's key (d = 32dt + 8g + 4h + i)
   __device__ __forceinline__ void store_rows(uint16_t* dKg, uint16_t* dVg) {
 #pragma unroll
@@ -180,11 +206,19 @@ struct DkdvWave {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * dt + 8 * g + 4 * h;
-        if (D == 64) {  // dK was carried times 8 (see ds_pair); the division is exact
-          for (int u = 2 * g; u < 2 * g + 2; ++u) dKp[dt][u] = pack_bf16(bf_lo(dKp[dt][u]) * 0.125f, bf_hi(dKp[dt][u]) * 0.125f);
+        // D = 64: dK was carried times 8 (see ds_pair); the division is exact
+        if constexpr (F32S) {
+          const f32x16& k_ = st32[C::DT + dt];
+          const f32x16& v_ = st32[dt];
+          *(u32x2*)(dKg + d0) = u32x2{pack_bf16(k_[4 * g] * 0.125f, k_[4 * g + 1] * 0.125f),
+                                      pack_bf16(k_[4 * g + 2] * 0.125f, k_[4 * g + 3] * 0.125f)};
+          *(u32x2*)(dVg + d0) = u32x2{pack_bf16(v_[4 * g], v_[4 * g + 1]), pack_bf16(v_[4 * g + 2], v_[4 * g + 3])};
+        } else {
+          if (D == 64)
+            for (int u = 2 * g; u < 2 * g + 2; ++u) dKp[dt][u] = pack_bf16(bf_lo(dKp[dt][u]) * 0.125f, bf_hi(dKp[dt][u]) * 0.125f);
+          *(u32x2*)(dKg + d0) = u32x2{dKp[dt][2 * g], dKp[dt][2 * g + 1]};
+          *(u32x2*)(dVg + d0) = u32x2{dVp[dt][2 * g], dVp[dt][2 * g + 1]};
         }
-        *(u32x2*)(dKg + d0) = u32x2{dKp[dt][2 * g], dKp[dt][2 * g + 1]};
-        *(u32x2*)(dVg + d0) = u32x2{dVp[dt][2 * g], dVp[dt][2 * g + 1]};
       }
   }
 
@@ -309,7 +343,10 @@ struct DkdvWave {
       } else {
         const int k = i - 4 * C::KC, n = k / 4, j = k % 4;
         const uint32_t* src = n >= C::DT ? dS : Pp;
-        acc[n & 1] = mfma(op, u32x4{src[4 * j], src[4 * j + 1], src[4 * j + 2], src[4 * j + 3]}, acc[n & 1]);
+        if constexpr (F32S)
+          st32[n] = mfma(op, u32x4{src[4 * j], src[4 * j + 1], src[4 * j + 2], src[4 * j + 3]}, st32[n]);
+        else
+          acc[n & 1] = mfma(op, u32x4{src[4 * j], src[4 * j + 1], src[4 * j + 2], src[4 * j + 3]}, acc[n & 1]);
       }
       // vector work of this slot
       const Work w = work(i);
@@ -322,7 +359,16 @@ struct DkdvWave {
           ds_pair(w.t ? x1 : x0, w.t ? y1 : y0, w.t, w.u0 + v, st[2 * v], st[2 * v + 1]);
       }
       if (Sink::kOn && i < 4 && prev.on()) prev.store(i, dS);  // previous tile's dS (rewritten from slot 2KC on)
-      if (i < C::KC) {
+      if constexpr (F32S) {
+        // the previous tile's last chain rounded in the first KC slots, chain n - 1 while chain n
+        // runs (its first two query steps)
+        if (i < C::KC) {
+          round_chain(2 * C::DT - 1, (i * 16) / C::KC, ((i + 1) * 16) / C::KC);
+        } else if (i >= 4 * C::KC) {
+          const int k = i - 4 * C::KC, n = k / 4, j = k % 4;
+          if (n >= 1 && j < 2) round_chain(n - 1, 8 * j, 8 * j + 8);
+        }
+      } else if (i < C::KC) {
         // the previous tile's last chain (dK of d tile DT-1, block 1) back into the state
         pack_pairs(2 * C::DT - 1, (i * 8) / C::KC, ((i + 1) * 8) / C::KC);
       } else if (i >= 3 * C::KC && i < 4 * C::KC) {
@@ -344,10 +390,11 @@ struct DkdvWave {
   }
 };
 
-// D = 64: three workgroups per CU (168 VGPRs, a few spilled outside the product loop), 6-8%
-// faster than two; D = 128 needs its 244-253 VGPRs and runs two.
+// D = 64 without the dS store: three workgroups per CU (168 VGPRs, a few spilled outside the
+// product loop), 6-8% faster than two. D = 64 with the dS store: two workgroups per CU and the
+// fp32 dK/dV state. D = 128 needs its 244-253 VGPRs and runs two.
 template <int D, bool DS>
-__global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(256, (D == 64 && !DS) ? 3 : 2) bwd_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
 
@@ -369,7 +416,7 @@ __global__ void __launch_bounds__(256, D == 64 ? 3 : 2) bwd_kernel(BwdArgs a) {
   const int kw = k0 + 32 * wave;  // the wave's first key
   const bool wave_keys = kw < a.T;  // false only in the last block when T % 128 == 64
   const int key = kw + (lane & 31);
-  DkdvWave<D> wv;
+  DkdvWave<D, D == 64 && DS> wv;
   wv.init(lane, key, a.scale);
   wv.load_rows(a.k + base, a.v + base, min(key, a.T - 1), rs);  // rows past T are read in bounds, never stored
 
@@ -551,7 +598,7 @@ __global__ void __launch_bounds__(512, 1) bwd_short_kernel(BwdArgs a) {
 
   int pair = blockIdx.x;
   if (pair >= npairs) return;
-  DkdvWave<D> wv;
+  DkdvWave<D, true> wv;
   wv.init(lane, key, a.scale);
   for (int t = 0; t < nqt; ++t) issue_tile(pair, t);
   if (g >= 0) wv.load_rows(a.k + base_of(pair), a.v + base_of(pair), key, rs);
