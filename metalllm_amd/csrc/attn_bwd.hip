@@ -11,15 +11,16 @@
 // when the caller provides a workspace (flashAttentionBackwardWorkspace), this kernel also
 // stores every dS tile it computes, bf16, and attn_bwd_dqs.hip computes dQ = dS.K from them.
 //
-// Work split: 4 waves x 32 keys per workgroup, two workgroups per CU (three at D = 64). Wave w
-// owns keys 32w..32w+31 of the block: it keeps their K and V rows in registers as matrix-core
-// B operands and computes S and dP with lane = key (the query tile's Q and dO rows are A
-// operands from LDS), so P and dS come out of the accumulators already laid out as the B
+// Work split: 4 waves x 32 keys per workgroup, two workgroups per CU (three at D = 64 without the
+// dS store). Wave w owns keys 32w..32w+31 of the block: it keeps their K and V rows in registers
+// as matrix-core B operands and computes S and dP with lane = key (the query tile's Q and dO rows
+// are A operands from LDS), so P and dS come out of the accumulators already laid out as the B
 // operands of dV^T += dO^T.P and dK^T += Q^T.dS: no LDS round trip. dO^T and Q^T are read with
-// ds_read_b64_tr_b16 from the row-major tiles, four queries per read, in the order
-// {8g + 4h + i} that lane half h holds. Between query tiles dK and dV are bf16 values (the
-// reference stores them as bf16 after every query tile), carried packed two per register and
-// widened to fp32 for one 32-row d slice at a time.
+// ds_read_b64_tr_b16 from the row-major tiles, four queries per read, in the order {8g + 4h + i}
+// that lane half h holds. Between query tiles dK and dV are bf16 values (the reference stores
+// them as bf16 after every query tile), carried packed two per register and widened to fp32 for
+// one 32-row d slice at a time, or (D = 64 with the dS store, and the fused short-sequence
+// kernel) held as bf16-exact fp32 values and rounded in place.
 //
 // Per query tile: S and dP of query rows 0-31, their p, P and dS, the same for rows 32-63, then
 // the dK/dV products. Query tiles stream through LDS two stages deep by
