@@ -59,7 +59,7 @@ struct FwdCfg {
 template <int D>
 struct FwdState {
   f32x16 O[D / 32];
-  float m_use, l_run, alpha;
+  float m_run, l_run, alpha;  // running max of the rounded scores (units u), row sum, rescale factor
   bool rescale;
 };
 
@@ -304,15 +304,15 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
           // scores (exact reference point: the largest score's exponential is exactly 1)
           float mt = bf_lo(pack_bf16(max_halves(fmaxf(mxa, mxb)), 0.0f));
           if (D != 64) mt = bf_lo(pack_bf16(mt * a.scale, 0.0f));
-          // the exact running max; true on the first tile (m_use = -inf), false for a row whose
+          // the exact running max; true on the first tile (m_run = -inf), false for a row whose
           // keys in this tile are all masked (mt = -inf; a row always sees key 0 in tile 0)
-          const bool need = mt > st.m_use;
+          const bool need = mt > st.m_run;
           st.rescale = __any(need);
-          const float m_new = need ? mt : st.m_use;
-          st.alpha = exp2_hw((st.m_use - m_new) * c1);  // exactly 1 where m stays, 0 on the first tile
+          const float m_new = need ? mt : st.m_run;
+          st.alpha = exp2_hw((st.m_run - m_new) * c1);  // exactly 1 where m stays, 0 on the first tile
           st.l_run *= st.alpha;
-          st.m_use = m_new;
-          mb = st.m_use * c1;
+          st.m_run = m_new;
+          mb = st.m_run * c1;
         }
 #pragma unroll
         for (int p = 0; p < 16; ++p) {
@@ -379,7 +379,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   for (;;) {
 #pragma unroll
     for (int i = 0; i < C::DT; ++i) st.O[i] = zero16();
-    st.m_use = -INFINITY;
+    st.m_run = -INFINITY;
     st.l_run = 0.0f;
     st.alpha = 1.0f;
     st.rescale = false;
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
           w[1] = pack_bf16(st.O[dt][4 * g + 2] * inv, st.O[dt][4 * g + 3] * inv);
           *(u32x2*)(Og + d0) = w;
         }
-      if (h == 0) a.lse[(size_t)pair * a.T + q] = st.m_use * su + logf(lt);
+      if (h == 0) a.lse[(size_t)pair * a.T + q] = st.m_run * su + logf(lt);
     }
     if (!more) break;
     so = so_next;
