@@ -96,7 +96,7 @@ __host__ __device__ inline bool fwd_item_of(int bid, int grid, int k, int npairs
 }
 
 constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
-constexpr int kFwdPersistT = 256;  // sequences up to this length run the persistent forward
+constexpr int kFwdPersistT = 2048;  // sequences up to this length run the persistent forward
 constexpr int kBwdBlockN = 128;  // keys owned by one dK/dV workgroup
 constexpr int kDqBlockM = 128;   // query rows owned by one dQ workgroup
 constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)
