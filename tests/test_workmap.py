@@ -1,7 +1,11 @@
 """Workgroup -> (head pair, block) decode of both kernels (host function shared with the device
 code): every block of every (batch, head) pair is owned by exactly one workgroup, so dK/dV rows
 (backward) and O rows (forward) have a single writer; blocks of one pair share an XCD when the
-pair count allows; the largest causal blocks are dispatched first."""
+pair count allows; pairs go out in chunks whose blocks are dispatched block-major, largest causal
+work first, so that a greedy dispatcher that starts workgroups in id order as slots free up
+finishes within one block's work of the lower bound."""
+import heapq
+
 import numpy as np
 import pytest
 
@@ -26,13 +30,34 @@ def test_partition(B, T, H, D, kind, blk, last_first):
     if npairs % 8 == 0:  # workgroup i runs on XCD i % 8: all blocks of a pair share one XCD
         for p in range(npairs):
             assert len(set((np.nonzero(wm[:, 0] == p)[0] % 8).tolist())) == 1
+    # per dispatch group (an XCD's share when the pairs split over 8, else the whole grid): a chunk
+    # of C pairs, C * nblk >= one round of resident workgroups (64 per XCD), is dispatched with
+    # non-increasing work, and a chunk's pairs are consecutive in the group
+    groups = [np.arange(x, len(wm), 8) for x in range(8)] if npairs % 8 == 0 else [np.arange(len(wm))]
+    rnd = 64 if npairs % 8 == 0 else 512
+    C = max(1, -(-rnd // nblk))
+    for ids in groups:
+        w, pr = work[ids], wm[ids, 0]
+        for c0 in range(0, len(ids), C * nblk):
+            assert (np.diff(w[c0:c0 + C * nblk]) <= 0).all()
+            assert len(set(pr[c0:c0 + C * nblk].tolist())) == min(C, len(set(pr.tolist())) - c0 // nblk)
+        # greedy dispatch in id order onto one round of slots, block time = its work + 1 (start
+        # cost): no later than dispatching the same pairs one after another, each pair's blocks
+        # longest first
+        def makespan(ws):
+            slots = [0.0] * min(rnd, len(ws))
+            for d in ws:
+                heapq.heappush(slots, heapq.heappop(slots) + d + 1.0)
+            return max(slots)
+        pair_major = np.concatenate([np.sort(w[pr == p])[::-1] for p in sorted(set(pr.tolist()))])
+        assert makespan(w) <= makespan(pair_major)
 
 
 @pytest.mark.parametrize("B,T,H,D", [(128, 256, 6, 64), (16, 256, 6, 64), (3, 192, 5, 128), (1, 64, 1, 64),
                                      (2, 128, 3, 64)])
 @pytest.mark.parametrize("grid", [768, 512, 96, 8, 7, 1])
 def test_persistent_forward_items(B, T, H, D, grid):
-    """The persistent forward (T <= 256): every (pair, query block) item is run by exactly one
+    """The persistent forward (T <= 2048): every (pair, query block) item is run by exactly one
     workgroup; when the pair count and the grid are multiples of 8, all items of a workgroup
     belong to pairs on its XCD (workgroup w runs on XCD w % 8); each workgroup's causal work
     (query block + 1 key tiles per item) is within one item's work of the mean."""
