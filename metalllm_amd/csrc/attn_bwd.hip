@@ -403,7 +403,7 @@ __global__ void __launch_bounds__(256, (D == 64 && !DS) ? 3 : 2) bwd_kernel(BwdA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (a.T + C::BN - 1) / C::BN;
   int pair, kb;
-  decode_workgroup(blockIdx.x, a.B * a.H, nkb, false, pair, kb);
+  decode_workgroup(blockIdx.x, a.B * a.H, nkb, false, kBwdDispatchRound, pair, kb);
   const int b = pair / a.H, hd = pair - b * a.H;
   const int rs = a.H * D;
   const size_t base = ((size_t)b * a.T * a.H + hd) * D;

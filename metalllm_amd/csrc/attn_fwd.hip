@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(FwdArgs a) {
   if (PERSIST) {
     if (!fwd_item_of(blockIdx.x, gridDim.x, 0, a.B * a.H, nqb, pair, qb)) return;
   } else {
-    decode_workgroup(blockIdx.x, a.B * a.H, nqb, true, pair, qb);
+    decode_workgroup(blockIdx.x, a.B * a.H, nqb, true, kFwdDispatchRound, pair, qb);
   }
   size_t base;
   const uint16_t* Qg;

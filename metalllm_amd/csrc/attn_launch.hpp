@@ -59,10 +59,13 @@ hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s); // dQ fr
 bool backward_is_short(int T, int D);
 hipError_t launch_backward_short(const BwdArgs& a, bool accumulate, hipStream_t s);
 
-// Workgroups resident at once in one XCD's share of a grid: two per CU on the 32 CUs of an
-// MI355X XCD (the dK/dV and forward kernels at D = 128 and the stored-dS dK/dV kernel at D = 64;
-// the three-per-CU kernels use the same figure).
-constexpr int kDispatchRound = 64;
+// Dispatch chunk sizes, in workgroups per XCD group. The backward's is one round of resident
+// workgroups: two per CU on the 32 CUs of an MI355X XCD (the three-per-CU D = 64 kernels use the
+// same figure). The forward's is two rounds: measured at T = 4096, D = 128 with one round per
+// chunk, two and four, the forward took 1.345, 1.275 and 1.29 ms and the dK/dV kernel 2.31,
+// 2.39 and 2.37 ms.
+constexpr int kFwdDispatchRound = 128;
+constexpr int kBwdDispatchRound = 64;
 
 // Pairs per dispatch chunk: enough that one chunk's blocks fill a round of resident workgroups.
 __host__ __device__ inline int dispatch_chunk(int nblk, int group_slots) {
@@ -72,20 +75,21 @@ __host__ __device__ inline int dispatch_chunk(int nblk, int group_slots) {
 
 // Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
 // spread so that every block of one pair lands on the same XCD (workgroups are handed to the
-// 8 XCDs round-robin by id). A group's pairs are taken in chunks of dispatch_chunk pairs; inside
+// 8 XCDs round-robin by id). A group's pairs are taken in chunks of dispatch_chunk(nblk, round)
+// pairs (round: workgroups per XCD group, kFwdDispatchRound or kBwdDispatchRound); inside
 // a chunk the blocks go out block-major, the largest causal work first, across the chunk's pairs:
 //   forward : block = query block, longest (last) first
 //   backward: block = key block, longest (first) first
 // The hardware starts workgroups in id order as slots free up, so the long blocks of the last
 // pairs no longer start late and run alone at the end (pair by pair, the tail was up to one long
 // block), while the workgroups running at once still share a few pairs' tiles in L2.
-__host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, bool last_first, int& pair,
-                                                 int& blk) {
+__host__ __device__ inline void decode_workgroup(int bid, int npairs, int nblk, bool last_first, int round,
+                                                 int& pair, int& blk) {
   const bool grouped = (npairs & 7) == 0;  // 8 groups, one per XCD
   const int g = grouped ? 8 : 1;
   const int x = grouped ? (bid & 7) : 0, slot = grouped ? (bid >> 3) : bid;
   const int npx = npairs / g;  // pairs of this group
-  const int C = dispatch_chunk(nblk, grouped ? kDispatchRound : 8 * kDispatchRound);
+  const int C = dispatch_chunk(nblk, grouped ? round : 8 * round);
   const int chunk = slot / (C * nblk);
   const int r = slot - chunk * C * nblk;
   const int cc = C < npx - chunk * C ? C : npx - chunk * C;  // pairs in this chunk (the last may be short)
