@@ -310,7 +310,8 @@ const char* metalllmAttnErrorString(int code);
 int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_t count);
 
 /* Test hook (no counterpart in the reference): the item assignment of the persistent forward
- * that flashAttentionForward runs for M <= 2048 (one workgroup per resident slot, each taking
+ * that flashAttentionForward runs when B*NH*ceil(M/128) is at most twice the number of workgroups
+ * resident at once (one workgroup per resident slot, each taking
  * (pair, query block) items in turn), for a grid of `grid` workgroups: writes, for workgroup
  * w = 0..grid-1 in turn and each of its items in the order it runs them, the triple
  * (w, pair, block) into out[3*i..3*i+2], at most `count` items. Returns the number of items of

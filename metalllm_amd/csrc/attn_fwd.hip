@@ -491,11 +491,11 @@ void forward_prepare() {
 hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s) {
   const int nqb = (a.T + kFwdBlockM - 1) / kFwdBlockM;
   const int items = a.B * a.H * nqb;
-  if (a.T <= kFwdPersistT) {
+  const int res = D == 64 ? fwd_resident<64>() : fwd_resident<128>();
+  if (res <= 0) return hipErrorInvalidDevice;
+  if (items <= kFwdPersistItems * res) {
     // as many workgroups as are resident at once (a multiple of 8, so that pairs keep to one
     // XCD), or one per item when there are fewer items
-    const int res = D == 64 ? fwd_resident<64>() : fwd_resident<128>();
-    if (res <= 0) return hipErrorInvalidDevice;
     int grid = std::min(items, res);
     if (grid >= 8) grid -= grid % 8;
     if (D == 64)

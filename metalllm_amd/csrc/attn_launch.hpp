@@ -116,7 +116,13 @@ __host__ __device__ inline bool fwd_item_of(int bid, int grid, int k, int npairs
 }
 
 constexpr int kFwdBlockM = 128;  // query rows per forward workgroup
-constexpr int kFwdPersistT = 2048;  // sequences up to this length run the persistent forward
+// The forward runs persistent (each resident workgroup takes items in turn, the next item's first
+// tiles loaded during the current item's last step) when there are at most this many (pair, query
+// block) items per resident workgroup; with more, one workgroup per item in the chunked dispatch
+// order balances better. Measured: persistent faster at two items per slot (config 1, and config
+// 4's attention, 0.0855 against 0.090 ms), one workgroup per item faster at four (config 2,
+// 0.110 against 0.1155 ms) and at sixteen (T = 4096, D = 128).
+constexpr int kFwdPersistItems = 2;
 constexpr int kBwdBlockN = 128;  // keys owned by one dK/dV workgroup
 constexpr int kDqBlockM = 128;   // query rows owned by one dQ workgroup
 constexpr int kTile = 64;        // the reference's TILE_M = TILE_N (attention.metal:14-15)

@@ -110,17 +110,19 @@ def test_config1_slice_equals_config0(gpu):
     assert np.array_equal(out[:16], out0) and np.array_equal(lse[:16], lse0)
 
 
-@pytest.mark.parametrize("B,H,D,Tp", [(128, 6, 64, 256), (100, 3, 64, 192), (97, 3, 64, 64), (8, 3, 128, 256),
-                                      (32, 12, 64, 1024), (4, 4, 128, 2048)])
+@pytest.mark.parametrize("B,H,D,Tp", [(128, 6, 64, 256), (100, 3, 64, 192), (97, 3, 64, 64), (64, 3, 128, 256),
+                                      (8, 12, 64, 2048), (16, 4, 128, 2048)])
 def test_persistent_forward_equals_per_item_forward(gpu, B, H, D, Tp):
-    """Sequences of T <= 2048 run the persistent forward (each workgroup takes several (pair, query
-    block) items, the next item's Q rows and first K tiles loaded during the current item's last
-    step); longer ones one workgroup per item. Causal rows 0..Tp-1 of a T = 2112 sequence depend
-    only on keys 0..Tp-1 and visit the same key tiles in the same order, so the T = 2112 forward
-    (per item) and the T = Tp forward of the prefix (persistent) must agree bit for bit on those
-    rows. At B = 128, H = 6, T = 256 each workgroup takes two items; 300 and 291 pairs are not
-    multiples of 8 (one group of workgroups), at Tp = 64 an item has one key tile, and the T = 1024
-    case is config 2's shape (four items of different lengths per workgroup)."""
+    """The forward runs persistent (each workgroup takes several (pair, query block) items, the next
+    item's Q rows and first K tiles loaded during the current item's last step) when there are at
+    most two items per resident workgroup (768 at D = 64, 512 at D = 128 on MI355X), otherwise one
+    workgroup per item. Causal rows 0..Tp-1 of a T = 2112 sequence depend only on keys 0..Tp-1
+    and visit the same key tiles in the same order, so the T = 2112 forward (one workgroup per
+    item: its 17 query blocks per pair exceed two per slot in every case here) and the T = Tp
+    forward of the prefix (persistent) must agree bit for bit on those rows. At B = 128, H = 6,
+    T = 256 each workgroup takes two items; 300 and 291 pairs are not multiples of 8 (one group of
+    workgroups), at Tp = 64 an item has one key tile, and the T = 2048 cases are config 4's
+    attention shape and its D = 128 counterpart (exactly two items per slot)."""
     print(f"case B={B} H={H} D={D} Tp={Tp}", flush=True)
     q, k, v, _ = make_inputs(B, 2112, H, D, 61)
     out_l, lse_l = gpu_forward(q, k, v, gpu)

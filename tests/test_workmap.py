@@ -58,7 +58,7 @@ def test_partition(B, T, H, D, kind, blk, last_first):
                                      (2, 128, 3, 64)])
 @pytest.mark.parametrize("grid", [768, 512, 96, 8, 7, 1])
 def test_persistent_forward_items(B, T, H, D, grid):
-    """The persistent forward (T <= 2048): every (pair, query block) item is run by exactly one
+    """The persistent forward (at most two items per resident workgroup): every (pair, query block) item is run by exactly one
     workgroup; when the pair count and the grid are multiples of 8, all items of a workgroup
     belong to pairs on its XCD (workgroup w runs on XCD w % 8); each workgroup's causal work
     (query block + 1 key tiles per item) is within one item's work of the mean."""
