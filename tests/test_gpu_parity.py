@@ -409,3 +409,29 @@ def test_backward_parts_equal_flash_attention_backward(gpu):
             res.append((dQ, dK, dV))
         for a, b in zip(*res):
             assert torch.equal(a, b)
+
+
+def test_batch_split_is_bit_identical(gpu):
+    """Every (batch, head) pair is computed by its own workgroups, so the outputs of one batch must
+    not depend on the grid around it. At B = 25, H = 8, T = 1024, D = 64 (200 pairs, 25 per XCD
+    group) the forward runs one workgroup per item and the backward kernels run their grids in the
+    chunked dispatch order with a short last chunk (forward chunks of 16 pairs: 16 + 9; dK/dV
+    chunks of 8: 8 + 8 + 8 + 1); a single batch (8 pairs, one per XCD group) runs the persistent
+    forward and one-pair chunks. Batches 0, 12 and 24 run alone must give the same O, LSE, D and
+    gradients bit for bit, on both backward entry points."""
+    B, T, H, D = 25, 1024, 8, 64
+    print(f"case B={B} T={T} H={H} D={D} seed=71 against single batches 0, 12, 24", flush=True)
+    q, k, v, g = make_inputs(B, T, H, D, 71)
+    out, lse = gpu_forward(q, k, v, gpu)
+    Dv = gpu_compute_d(g, out, gpu)
+    full = [gpu_backward(g, Dv, lse, q, k, v, gpu, workspace=w) for w in (False, True)]
+    for b in (0, 12, 24):
+        one = lambda x: np.ascontiguousarray(x[b:b + 1])
+        out1, lse1 = gpu_forward(one(q), one(k), one(v), gpu)
+        assert np.array_equal(out1, out[b:b + 1]) and np.array_equal(lse1, lse[b:b + 1])
+        D1 = gpu_compute_d(one(g), out1, gpu)
+        assert np.array_equal(D1, Dv[b:b + 1])
+        for w, grads in zip((False, True), full):
+            got = gpu_backward(one(g), D1, lse1, one(q), one(k), one(v), gpu, workspace=w)
+            for x, y in zip(got, grads):
+                assert np.array_equal(x, y[b:b + 1])
