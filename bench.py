@@ -106,7 +106,7 @@ def bench_sublayer(args):
     computeD -> flashAttentionBackward -> computeGradDx/Dw (model.h:446-482, 621-690), with the
     accumulated gradients starting from zero (model.h:549-555). The per-call chain (timed per phase
     by events) zeroes them and adds into them; the headline, the phase encoder, writes them as
-    0 + the gradient. Reports ms per step and the attention share."""
+    0 + the gradient. Returns the result object (ms per step and the attention share)."""
     import torch
     import metalllm_amd as M
     from metalllm_amd import sublayer as S
@@ -184,7 +184,8 @@ def bench_sublayer(args):
         dst.copy_(src)
         torch.cuda.synchronize()
     ms = ms_encode
-    result = {
+    sub.close()
+    return {
         "metric": "attention sublayer fwd+bwd ms per step (config 4), with the attention share",
         "value": round(ms, 4),
         "unit": "ms",
@@ -208,34 +209,28 @@ def bench_sublayer(args):
                    "gemms": round(gemm_flop / ((total_events - attn - phase["zero"]) * 1e-3) / 1e12, 2),
                    "attention": round(attn_flop / (attn * 1e-3) / 1e12, 2)},
     }
-    print(json.dumps(result), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4],
-                    help="1-3: attention core (fwd + computeD + bwd); 4: the whole attention sublayer")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="after the timed steps, run one device copy of 256 MiB (read) -> 256 MiB (write), "
-                         "the known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
-    args = ap.parse_args()
+def step_bound_ms(B, H, T, D):
+    """Roofline time of one attention step (fwd + computeD + bwd): per kernel the larger of its
+    algorithmic bytes at 8 TB/s and its causal FLOPs at the dense bf16 peak, summed."""
+    bthd, bht = B * T * H * D, B * H * T
+    ff, fb = flops(B, H, T, D)
+    fwd = max((8 * bthd + 4 * bht) / PEAK_HBM_GBS / 1e9, ff / PEAK_BF16_TFLOPS / 1e12)
+    cd = (4 * bthd + 4 * bht) / PEAK_HBM_GBS / 1e9
+    bwd = max((16 * bthd + 8 * bht) / PEAK_HBM_GBS / 1e9, fb / PEAK_BF16_TFLOPS / 1e12)
+    return 1e3 * (fwd + cd + bwd), 1e3 * fwd, 1e3 * bwd
 
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures the single-GPU hot path only: attention shards per (batch, head) with no "
-              "exchange, so this build runs and reports one GPU (use --gpus 1).", file=sys.stderr)
-        sys.exit(2)
 
+def run_core(cfg_id, steps, warmup, calibrate_copy=False):
+    """Times the attention core of one config (fwd + computeD + backward, inputs resident in HBM).
+    Two step kinds: the headline step with flashAttentionBackwardWorkspace (parts 2 and 3) and the
+    reference-contract step with flashAttentionBackward (parts 0 and 1, into a zeroed dQ, the
+    memset included). Returns the per-kernel event spans and both steps' spans."""
     import torch
     import metalllm_amd as M
 
-    if args.config == 4:
-        return bench_sublayer(args)
-    B, H, T, D, qk_scale, desc = CONFIGS[args.config]
+    B, H, T, D, qk_scale, desc = CONFIGS[cfg_id]
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -264,8 +259,8 @@ def main():
     # each kernel is timed by its own events. The workspace path writes dQ in full; the
     # recomputing path adds into dQ (the reference's contract), so its steps zero dQ first.
     # ev: None (untimed), 5 events (a marker before, between and after the kernels: the phase
-    # spans) or 2 events (start and end only: the headline step span, free of the markers'
-    # own cost, which is a few microseconds each)
+    # spans) or 2 events (start and end only: the step span, free of the markers' own cost,
+    # which is a few microseconds each)
     def step(ev=None, parts=(2, 3)):
         flush.fill_(parts[0])
         mark = (lambda i: ev[i].record(stream)) if ev is not None and len(ev) == 5 else (lambda i: None)
@@ -283,52 +278,120 @@ def main():
         if ev is not None:
             ev[-1].record(stream)
 
-    # the recomputing backward, for comparison (its own warmup and events)
+    def timed_steps(parts, n, nev):
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(n)]
+        for e in evs:
+            step(e, parts=parts)
+        torch.cuda.synchronize()
+        return evs
+
+    # the reference-contract step (flashAttentionBackward): its own warmup, phase and step spans
+    n_rc = max(3, steps // 4)
     for _ in range(2):
         step(parts=(0, 1))
-    rc_events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(max(3, args.steps // 4))]
-    for e in rc_events:
-        step(e, parts=(0, 1))
-    torch.cuda.synchronize()
+    rc_events = timed_steps((0, 1), n_rc, 5)
+    rc_plain = timed_steps((0, 1), n_rc, 2)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-
     # phase spans: steps with markers between the kernels
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        step(events[i])
-    torch.cuda.synchronize()
+    events = timed_steps((2, 3), steps, 5)
     # headline: the same steps with one event pair each
-    plain = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(plain[i])
-    torch.cuda.synchronize()
+    plain = timed_steps((2, 3), steps, 2)
     wall = time.perf_counter() - t0
 
-    if args.calibrate_copy:
+    if calibrate_copy:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
 
-    # per-kernel times from the events
     span = lambda a, b, evs=events: sorted(e[a].elapsed_time(e[b]) for e in evs)
-    fwd_ms, cd_ms, kv_ms, dq_ms, bwd_ms = span(0, 1), span(1, 2), span(2, 3), span(3, 4), span(2, 4)
+    res = {
+        "shape": (B, H, T, D, qk_scale, desc), "ws_bytes": ws_bytes,
+        "fwd": span(0, 1), "cd": span(1, 2), "kv": span(2, 3), "dq": span(3, 4), "bwd": span(2, 4),
+        "marked": span(0, 4), "step": span(0, 1, plain), "wall_ms": wall * 1e3 / steps,
+        "rc_kv": span(2, 3, rc_events), "rc_dq": span(3, 4, rc_events), "rc_bwd": span(2, 4, rc_events),
+        "rc_step": span(0, 1, rc_plain),
+    }
+    del q, k, v, dO, flush, out, lse, Dv, dQ, dK, dV, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def med(xs):
+    return xs[len(xs) // 2]
+
+
+def core_summary(cfg_id, r):
+    """Compact per-config record (the extra configs of the default run)."""
+    B, H, T, D, qk_scale, desc = r["shape"]
+    ff, fb = flops(B, H, T, D)
+    bound, bound_f, bound_b = step_bound_ms(B, H, T, D)
+    ms, rc_ms = med(r["step"]), med(r["rc_step"])
+    regime = "hbm" if cfg_id == 1 else ("ridge" if cfg_id == 2 else "mfma")
+    return {
+        "workload": f"config{cfg_id}: causal attention fwd+computeD+bwd, {desc}",
+        "B": B, "H": H, "T": T, "D": D, "qk_scale": qk_scale,
+        "ms_per_step": round(ms, 4),
+        "tflops": round((ff + fb) / (ms * 1e-3) / 1e12, 2),
+        "pct_of_peak": round(100.0 * (ff + fb) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "bound": {"regime": regime, "step_ms": round(bound, 4), "fwd_ms": round(bound_f, 4),
+                  "bwd_ms": round(bound_b, 4),
+                  "note": "per kernel max(algorithmic bytes / 8 TB/s, causal FLOPs / 2516.6 TFLOP/s), summed "
+                          "over fwd, computeD and bwd"},
+        "frac_of_bound": round(bound / ms, 4),
+        "phases_ms_median": {"fwd": round(med(r["fwd"]), 4), "computeD": round(med(r["cd"]), 4),
+                             "bwd": round(med(r["bwd"]), 4), "bwd_dkdv": round(med(r["kv"]), 4),
+                             "bwd_dq": round(med(r["dq"]), 4)},
+        "ref_contract_step": {"ms_per_step": round(rc_ms, 4),
+                              "tflops": round((ff + fb) / (rc_ms * 1e-3) / 1e12, 2),
+                              "bwd_ms_median": round(med(r["rc_bwd"]), 4)},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4],
+                    help="1-3: attention core (fwd + computeD + bwd); 4: the whole attention sublayer")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the other BASELINE configs that the default run measures beside the headline")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run one device copy of 256 MiB (read) -> 256 MiB (write), "
+                         "the known-size reference for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU hot path only: attention shards per (batch, head) with no "
+              "exchange, so this build runs and reports one GPU (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch  # noqa: F401
+    import metalllm_amd as M  # noqa: F401
+
+    if args.config == 4:
+        print(json.dumps(bench_sublayer(args)), flush=True)
+        return
+    r = run_core(args.config, args.steps, args.warmup, args.calibrate_copy)
+    B, H, T, D, qk_scale, desc = r["shape"]
+    ws_bytes = r["ws_bytes"]
+    fwd_ms, cd_ms, kv_ms, dq_ms, bwd_ms = r["fwd"], r["cd"], r["kv"], r["dq"], r["bwd"]
     avg = lambda xs: sum(xs) / len(xs)
-    med = lambda xs: xs[len(xs) // 2]
     ff, fb = flops(B, H, T, D)
     unit = B * H * T * T * D  # one causal T x T x D product over all (b, h)
     # headline: the median over the timed steps of each step's event span (one pair around the
     # kernels); the wall-clock mean of those steps (which also covers the cache flush between
     # steps) is reported beside it, and so is the span of the marked steps
-    ms_per_step = med(span(0, 1, plain))
-    marked_ms = med(span(0, 4))
-    wall_ms = wall * 1e3 / args.steps
+    ms_per_step = med(r["step"])
+    marked_ms = med(r["marked"])
     value = (ff + fb) / (ms_per_step * 1e-3) / 1e12
     # dominant kernel: the dK/dV kernel (4 products: S, dP, dV = P^T dO, dK = dS^T Q)
     kv_avg = avg(kv_ms)
@@ -338,7 +401,7 @@ def main():
     bthd = B * T * H * D
     dq_bytes = ws_bytes + 2 * bthd + 4 * bthd
     dq_avg = avg(dq_ms)
-    rc_kv, rc_dq, rc_bwd = span(2, 3, rc_events), span(3, 4, rc_events), span(2, 4, rc_events)
+    rc_kv, rc_dq, rc_bwd = r["rc_kv"], r["rc_dq"], r["rc_bwd"]
 
     if D == 64 and T <= 256:
         # short sequences: one fused kernel (part 2) computes dK, dV and dQ without the workspace
@@ -386,6 +449,7 @@ def main():
             "avg_ms": round(dq_avg, 4),
         }
 
+    rc_ms = med(r["rc_step"])
     result = {
         "metric": "causal attn fwd+bwd TFLOP/s at B,H,T,D bf16; % of MI355X bf16 MFMA peak",
         "value": round(value, 2),
@@ -405,7 +469,7 @@ def main():
         "timing": "median of per-step HIP event spans (one event pair around fwd, computeD and bwd); "
                   "512 MB written between steps (L2 and Infinity Cache flush); phases from as many steps "
                   "again with a marker between the kernels",
-        "wall_ms_per_step_incl_flush": round(wall_ms, 4),
+        "wall_ms_per_step_incl_flush": round(r["wall_ms"], 4),
         "marked_ms_per_step": round(marked_ms, 4),
         "phases": {
             "fwd_ms_median": round(med(fwd_ms), 4), "computeD_ms_median": round(med(cd_ms), 4),
@@ -418,10 +482,28 @@ def main():
             "bwd_tflops": round(fb / (med(bwd_ms) * 1e-3) / 1e12, 2),
             "computeD_gbs": round((4 * bthd + 4 * B * H * T) / (med(cd_ms) * 1e-3) / 1e9, 1),
         },
+        # the step the reference's own entry point gives (model.h:648-665): flashAttentionBackward
+        # (no workspace, dQ accumulated into a zeroed buffer, the memset timed with it)
+        "ref_contract_step": {
+            "ms_per_step": round(rc_ms, 4),
+            "tflops": round((ff + fb) / (rc_ms * 1e-3) / 1e12, 2),
+            "pct_of_peak": round(100.0 * (ff + fb) / (rc_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            "bwd_ms_median": round(med(rc_bwd), 4),
+        },
         "roofline": roofline,
     }
     if roofline_dq is not None:
         result["roofline_dq"] = roofline_dq
+    if not args.no_extra_configs:
+        # the other BASELINE configs, measured in the same run (the headline stays config 3)
+        extra = {}
+        for cid in sorted(CONFIGS):
+            if cid != args.config:
+                extra[f"config{cid}"] = core_summary(cid, run_core(cid, args.steps, args.warmup))
+        c4 = bench_sublayer(args)
+        extra["config4"] = {k: c4[k] for k in ("config", "ms_per_step", "step_mode", "modes_ms_per_step",
+                                               "attention_share", "phases_ms_median", "tflops")}
+        result["extra_configs"] = extra
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(B, H, T, D, qk_scale, args.cpu_threads)
     print(json.dumps(result), flush=True)

@@ -22,9 +22,17 @@
  * pass, no read of the old values). D holds the bf16-rounded value of rowsum(dO*O), stored as
  * fp32.
  *
- * Semantics: asynchronous on `stream` (NULL = the default stream); no allocation, no host
- * synchronisation, no global state, so calls on distinct streams may run concurrently (the
- * workspace variant's workspace belongs to one call at a time). Each
+ * Semantics: asynchronous on `stream` (NULL = the default stream); no allocation and no host
+ * synchronisation. Calls on distinct streams may run concurrently, with two exceptions: the
+ * workspace variant's workspace belongs to one call at a time, and flashAttentionBackwardNoAlloc
+ * calls on one GPU share that GPU's fixed dS array, so they must be serialised. Library state
+ * that outlives a call: (1) flashAttentionForward caches, per device, the number of its
+ * persistent workgroups resident at once (CU count times occupancy, from two device queries on
+ * the first forward call on that device; host memory, read-only afterwards); (2) the
+ * METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64 MiB) device array of flashAttentionBackwardNoAlloc,
+ * which the HIP runtime creates on every GPU where it loads the library's code object (at the
+ * first launch of any of its kernels there) and keeps until the process ends, whether or not that
+ * entry point is ever called. Each
  * entry point validates its arguments before touching the device and returns METALLLM_ATTN_OK or
  * a negative error code; a failed kernel launch returns METALLLM_ATTN_E_LAUNCH.
  * Supported shapes: M (= T) a positive multiple of 64, D in {64, 128}, N == NH*D, B >= 1,
@@ -116,9 +124,11 @@ int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const fl
  * with the dS tiles in a fixed per-device array of METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64 MiB,
  * held by every GPU the library runs on until the process ends) instead of a caller workspace.
  * Calls no hipMalloc/hipFree. Shapes whose metalllmAttnBackwardWorkspaceSize exceeds the array
- * return METALLLM_ATTN_E_SIZE (config 1, B = 128, NH = 6, M = 256, needs 60 MiB). All calls on
- * one GPU share the array: calls that overlap on one GPU race. The first call on a device looks
- * up the array's address there. */
+ * return METALLLM_ATTN_E_SIZE (e.g. B = 16, NH = 12, M = 512, D = 64 needs 56.6 MB and fits),
+ * except D = 64 with M <= 256 (the reference's own shape, config 1 included), which runs the fused
+ * short-sequence backward, stores no dS tiles and accepts any batch. All calls on one GPU share
+ * the array: calls that overlap on one GPU race. The first call on a device looks up the array's
+ * address there. */
 #define METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                                   const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,

@@ -47,7 +47,11 @@ extern "C" int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d,
   uint64_t need = 0;
   const int rc = metalllmAttnBackwardWorkspaceSize(p, &need);  // validates the shape
   if (rc) return rc;
-  if (need > kScratchBytes) return METALLLM_ATTN_E_SIZE;
+  // D = 64, M <= 256 runs the fused short-sequence backward, which keeps dS in LDS and never
+  // reads the workspace: any batch size fits there, and the nominal size is passed on so that the
+  // workspace entry point's own size check accepts it
+  const bool short_path = mla::backward_is_short((int)p->M, (int)p->D);
+  if (!short_path && need > kScratchBytes) return METALLLM_ATTN_E_SIZE;
   if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
   if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
@@ -55,5 +59,6 @@ extern "C" int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d,
   void* ws = nullptr;
   const int src = scratch_on_current_device(&ws);
   if (src) return src;
-  return flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, ws, kScratchBytes, p, stream);
+  return flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, ws, short_path ? need : kScratchBytes, p,
+                                         stream);
 }

@@ -25,6 +25,9 @@ PASS_SEQ8 = 0
 PASS_IL4 = 1
 BWD_REFERENCE = 0
 BWD_FP32 = 1
+DS_REFERENCE = 0
+DS_FUSED = 1
+DS_COUNT = 2
 
 # Tensor ids of the seeded input generator.
 TID_Q, TID_K, TID_V, TID_DO = 1, 2, 3, 4
@@ -38,7 +41,7 @@ class AttentionParams(ctypes.Structure):
 class OracleOpts(ctypes.Structure):
     _fields_ = [("threads", ctypes.c_int), ("b_begin", ctypes.c_int), ("b_end", ctypes.c_int),
                 ("gemm_model", ctypes.c_int), ("bwd_mode", ctypes.c_int), ("d_round", ctypes.c_int),
-                ("fwd_lazy", ctypes.c_float)]
+                ("fwd_lazy", ctypes.c_float), ("ds_form", ctypes.c_int)]
 
 
 def build(force: bool = False) -> str:
@@ -67,10 +70,13 @@ def params(B: int, T: int, H: int, D: int) -> AttentionParams:
 
 
 def opts(threads: int = 0, b_begin: int = 0, b_end: int = 0, gemm_model: int = GEMM_MFMA,
-         bwd_mode: int = BWD_REFERENCE, d_round: int = 1, fwd_lazy: float = 0.0) -> OracleOpts:
+         bwd_mode: int = BWD_REFERENCE, d_round: int = 1, fwd_lazy: float = 0.0, ds_form: int = 0) -> OracleOpts:
     """fwd_lazy > 0 is a diagnosis mode (a lazy softmax reference point that moves only by more
-    than fwd_lazy log2 units); 0 is the reference's exact running max, which the GPU forward uses."""
-    return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round, fwd_lazy)
+    than fwd_lazy log2 units); 0 is the reference's exact running max, which the GPU forward uses.
+    ds_form: DS_REFERENCE (the reference's order of dS = bf16(p*(dP - D)*scale)), DS_FUSED (the
+    D = 128 GPU kernels' p*fma(dP, scale, -D*scale)) or DS_COUNT (reference order, counting the
+    roundings the fused order would change: ds_flips())."""
+    return OracleOpts(threads, b_begin, b_end, gemm_model, bwd_mode, d_round, fwd_lazy, ds_form)
 
 
 def _check(rc: int, what: str):
@@ -95,6 +101,8 @@ class Oracle:
         L.oracle_fill_normal_bf16.restype = None
         L.oracle_dot.argtypes = [ctypes.c_float, f32p, f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.oracle_dot.restype = ctypes.c_float
+        L.oracle_ds_flips.argtypes = []
+        L.oracle_ds_flips.restype = ctypes.c_uint64
         self.lib = L
 
     def forward(self, q, k, v, o: OracleOpts | None = None):
@@ -177,6 +185,12 @@ def compute_d(dO, O, o: OracleOpts | None = None):
 
 def backward(dO, Dv, lse, q, k, v, o: OracleOpts | None = None):
     return default().backward(dO, Dv, lse, q, k, v, o)
+
+
+def ds_flips() -> int:
+    """dS values of the last backward call with ds_form=DS_COUNT whose bf16 rounding the fused
+    order p*fma(dP, scale, -D*scale) changes."""
+    return int(default().lib.oracle_ds_flips())
 
 
 def bf16_to_f32(x: np.ndarray) -> np.ndarray:

@@ -66,6 +66,12 @@ typedef struct {
 
 enum { GEMM_CHUNK16 = 0, GEMM_SEQ = 1, GEMM_MFMA = 2 };
 enum { BWD_REFERENCE = 0, BWD_FP32 = 1 };
+// dS = bf16(p*(dP - D)*scale) (attention.metal:284): DS_REFERENCE evaluates it in the reference's
+// order, (p*(dP - D))*scale, each product and difference rounded to fp32; DS_FUSED in the order the
+// GPU's D = 128 kernels use, p*fma(dP, scale, -fp32(D*scale)) (for D = 64 the scale is 1/8 and the
+// two orders agree exactly). DS_COUNT computes the reference order and counts, over the whole call,
+// the dS values whose bf16 rounding the fused order would change (oracle_ds_flips()).
+enum { DS_REFERENCE = 0, DS_FUSED = 1, DS_COUNT = 2 };
 
 typedef struct {
   int threads;      // worker threads (<=0: hardware_concurrency)
@@ -80,6 +86,7 @@ typedef struct {
                     // tile max exceeds it by more than t in log2 units (a lazy scheme a forward
                     // may use to skip O rescales); P = bf16(exp(s - m)) is then rounded relative
                     // to that point, away from the reference's rounding point
+  int ds_form;      // DS_REFERENCE, DS_FUSED or DS_COUNT (above)
 } OracleOpts;
 
 }  // extern "C"
@@ -384,7 +391,7 @@ void forward_head(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
 // flashAttentionBackward for one (b,h): attention.metal:219-298, every key tile in order.
 void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV, const AttentionParams& p, uint32_t b,
-                   uint32_t h, int model, int mode) {
+                   uint32_t h, int model, int mode, int ds_form, uint64_t* ds_flips) {
   const int T = (int)p.M, D = (int)p.D, ntiles = T / TILE;
   Mat Q, K, V, G, dS, Pt, dSt, Kt, Qt, Gt;
   gather_head(q, p, b, h, Q);
@@ -395,6 +402,7 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
   Pt.resize(TILE, TILE);
   dSt.resize(TILE, TILE);
   const float scale = 1.0f / std::sqrt((float)D);  // :268
+  uint64_t flips = 0;
   const float* lrow = lse + ((size_t)b * p.NH + h) * p.M;
   const float* drow = Dv + ((size_t)b * p.NH + h) * p.M;
   std::vector<float> dQacc((size_t)T * D, 0.0f), S((size_t)TILE * TILE), dP((size_t)TILE * TILE);
@@ -421,7 +429,14 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
           if (kt == qt && c > r) val = 0.0f;
           const float Pb = bf(val);
           const float t1 = val * (dP[(size_t)r * TILE + c] - ((ORACLE_MUTANT == 4) ? 0.0f : dv));
-          const float dsv = bf(t1 * scale);
+          float dsv = bf(t1 * scale);
+          if (ds_form != DS_REFERENCE) {
+            const float dsf = bf(val * std::fma(dP[(size_t)r * TILE + c], scale, -(dv * scale)));
+            if (ds_form == DS_FUSED)
+              dsv = dsf;
+            else
+              flips += (dsf != dsv);
+          }
           Pt.f[(size_t)c * TILE + r] = Pb;
           dS.f[(size_t)r * TILE + c] = dsv;
           dSt.f[(size_t)c * TILE + r] = dsv;
@@ -467,7 +482,10 @@ void backward_head(const uint16_t* dO, const float* Dv, const float* lse, const 
     float* qrow = dQ + ((size_t)b * p.M + t) * p.N + (size_t)h * D;
     for (int d = 0; d < D; ++d) qrow[d] += dQacc[(size_t)t * D + d];
   }
+  *ds_flips = flips;
 }
+
+std::atomic<uint64_t> g_ds_flips{0};
 
 }  // namespace
 
@@ -531,12 +549,21 @@ int oracle_backward(const uint16_t* dO, const float* Dv, const float* lse, const
   const Slice s = slice_of(*p, o);
   const int model = o ? o->gemm_model : GEMM_MFMA;
   const int mode = o ? o->bwd_mode : BWD_REFERENCE;
+  const int ds_form = o ? o->ds_form : DS_REFERENCE;
   const int nwork = (int)((s.b1 - s.b0) * p->NH);
+  g_ds_flips = 0;
   parallel_for(nwork, o ? o->threads : 0, [&](int i) {
-    backward_head(dO, Dv, lse, q, k, v, dQ, dK, dV, *p, s.b0 + (uint32_t)i / p->NH, (uint32_t)i % p->NH, model, mode);
+    uint64_t flips = 0;
+    backward_head(dO, Dv, lse, q, k, v, dQ, dK, dV, *p, s.b0 + (uint32_t)i / p->NH, (uint32_t)i % p->NH, model, mode,
+                  ds_form, &flips);
+    g_ds_flips += flips;
   });
   return 0;
 }
+
+// dS values of the last oracle_backward call with ds_form == DS_COUNT whose bf16 rounding the
+// fused order changes.
+uint64_t oracle_ds_flips(void) { return g_ds_flips.load(); }
 
 // Seeded counter-based N(0,1)*scale samples rounded to bf16, keyed by (seed, tensor id, flat
 // index of [b,t,h,d]). The flat index does not depend on B, so batch b of a larger-B draw equals

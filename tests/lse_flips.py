@@ -74,7 +74,24 @@ def diagnose_row(q, k, lse_a, lse_b, b, h, t, model_a, model_b, tol=5e-5):
         "row": (b, h, t), "flips": [int(j) for j in flips], "observed": observed, "explained": float(explained),
         "max_score_step": float(np.abs(sa - sb).max()) if len(flips) else 0.0,
         "flip_weight": float(w[flips].sum()) if len(flips) else 0.0,
+        "weights": [float(np.ravel(w)[j]) for j in flips],
+        "steps": [float(abs(np.ravel(sa)[j] - np.ravel(sb)[j])) for j in flips],
     }
+
+
+def o_move_bound(info, v_keys, o_row):
+    """Per-column bound on how far the flipped scores of one diagnosed row move its output
+    O = sum_i w_i V_i. Moving score j by delta multiplies its unnormalised weight by e^delta, which
+    changes O by w_j (e^delta - 1) (V_j - O) / (1 + w_j (e^delta - 1)); summed over the flips with
+    |e^delta - 1| <= e^|delta| - 1 and the denominator at its smallest. v_keys: the flipped keys' V
+    rows [n_flips, D]; o_row: the reference's unrounded O row [D]. w_j is the larger of the two
+    models' weights, so the bound holds from either side."""
+    w = np.asarray(info["weights"], np.float64)
+    st = np.asarray(info["steps"], np.float64)
+    den = 1.0 - float(np.sum(w * -np.expm1(-st)))
+    num = np.sum((w * np.expm1(st))[:, None] * np.abs(np.asarray(v_keys, np.float64) - np.asarray(o_row, np.float64)[None, :]),
+                 axis=0)
+    return num / den
 
 
 def rows_beyond(lse_a, lse_b, bar=1e-3):

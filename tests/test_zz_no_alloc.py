@@ -42,6 +42,9 @@ def test_no_alloc_backward_matches_workspace_backward(gpu):
     # short-sequence backward of T <= 256), then a smaller D = 128 input
     _run(gpu, 16, 512, 12, 64, 61)
     _run(gpu, 2, 512, 4, 128, 62)
+    # D = 64, T = 256 runs the fused short backward (dS in LDS, the array unused): accepted beyond
+    # the array's nominal size (120 MiB of tiles here)
+    _run(gpu, 256, 256, 6, 64, 63)
     import metalllm_amd as M
     with pytest.raises(M.AttentionError):  # tiles beyond the array: rejected before the device
         import torch
