@@ -26,9 +26,10 @@
  * synchronisation. Calls on distinct streams may run concurrently, with two exceptions: the
  * workspace variant's workspace belongs to one call at a time, and flashAttentionBackwardNoAlloc
  * calls on one GPU share that GPU's fixed dS array, so they must be serialised. Library state
- * that outlives a call: (1) flashAttentionForward caches, per device, the number of its
- * persistent workgroups resident at once (CU count times occupancy, from two device queries on
- * the first forward call on that device; host memory, read-only afterwards); (2) the
+ * that outlives a call: (1) two per-device caches in host memory, filled by device queries on the
+ * first call on that device and read-only afterwards: the number of flashAttentionForward's
+ * persistent workgroups resident at once (CU count times occupancy) and the CU count the dQ
+ * kernel of the workspace backward sizes its grid by; (2) the
  * METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64 MiB) device array of flashAttentionBackwardNoAlloc,
  * which the HIP runtime creates on every GPU where it loads the library's code object (at the
  * first launch of any of its kernels there) and keeps until the process ends, whether or not that

@@ -41,8 +41,13 @@
 // pair's blocks largest first, and dealt in snake order across its workgroups: workgroups
 // working at the same time share one or two pairs' K tiles, and every workgroup gets about the
 // same number of key steps. Stages run back to back across item boundaries, and an item's dQ is
-// stored straight from the accumulators (16-byte stores, row segments that L2 merges into whole
-// lines) while the next item's stages are computed. Every row of dQ is written once, in full.
+// stored straight from the accumulators while the next item's stages are computed. Every row of
+// dQ is written once, in full. The products are computed as dQ = dS.K (m = query position, n = d;
+// the same operand registers as dQ^T = K^T.dS^T, the same sums bit for bit) so that a lane holds
+// one d of 16 rows: each 4-byte store writes 32 consecutive d of a row per half wave, whole
+// 128-byte lines (with dQ^T each 16-byte store wrote 32-byte pieces of 32 rows; c3 1.047 ->
+// 1.015 ms, c2 0.113 -> 0.109 ms). The vmcnt waits saturate at 63: with 64 stores per item a
+// wait may also cover a few of them, which only waits longer.
 #include <algorithm>
 #include <atomic>
 
@@ -67,11 +72,11 @@ struct DqsCfg {
   static constexpr int CPW = KPW + DSPW;               // copy instructions per wave and stage
   static constexpr int MB = D / 64;                    // 32-row d blocks per wave
   static constexpr int DH = D / 2;                     // d columns per wave
-  static constexpr int NSTORE = MB * 2 * 4;            // dQ store instructions per wave and item
+  static constexpr int NSTORE = MB * 2 * 16;           // dQ store instructions per wave and item
   static constexpr int WG_PER_CU = NSTAGE * STAGE <= 80 * 1024 ? 2 : 1;
   static_assert(KINS % WAVES == 0, "K copies split evenly over the waves");
   static_assert(NSTAGE == 2 || NSTAGE == 3, "ring depth");
-  static_assert(CPW + 2 * NSTORE < 64, "vmcnt range");
+
 };
 
 // dma16 with the non-temporal hint: dS tiles are read once.
@@ -86,10 +91,11 @@ __device__ __forceinline__ u32x2 tr_at(uint32_t byte_addr) {
 
 // s_waitcnt takes an immediate: waits with the first of Ns equal to n, or with 0 (everything)
 // when none is.
+// (counts above 63, the counter's range, wait for everything but the last 63)
 template <int N, int... Rest>
 __device__ __forceinline__ void wait_vm_of(int n) {
   if (n == N) {
-    wait_vm<N>();
+    wait_vm<(N < 63 ? N : 63)>();
   } else {
     if constexpr (sizeof...(Rest) > 0)
       wait_vm_of<Rest...>(n);
@@ -221,7 +227,7 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
         const u32x2 lo = tr_at(ad), hi = tr_at(ad + 4 * 2 * D);
         const u32x4 A = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[m][nb] = mfma(A, Bo[nb], acc[m][nb]);
+        for (int nb = 0; nb < 2; ++nb) acc[m][nb] = mfma(Bo[nb], A, acc[m][nb]);  // dQ (m = query, n = d)
       }
     }
   };
@@ -280,19 +286,20 @@ dqs_kernel(BwdArgs a) {  // (THREADS, WG_PER_CU of DqsCfg)
     if (C::NSTAGE == 3) s2 = s1;
     s1 = false;
     if (++kt < cur.nk) continue;
-    // ---- item done: dQ = dQ^T of this wave, lane holds query position p = 32nb + l32 ----
+    // ---- item done: lane holds d = 32mm + l32 of query positions x = 8(r/4) + 4h + r%4 of block
+    // nb (position p = 32nb + x is query row 32(x/16) + 8((x/4)%4) + 4nb + x%4 of the tile); one
+    // store writes 32 consecutive d of one row per half wave: whole 128-byte lines ----
     if (wave_q) {
-      float* dQg = a.dQ + base_of(cur.pair) + (size_t)qtw * 64 * rs + wd * C::DH + 4 * h;
+      float* dQg = a.dQ + base_of(cur.pair) + (size_t)qtw * 64 * rs + wd * C::DH + l32;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int qin = 32 * (l32 >> 4) + 8 * ((l32 >> 2) & 3) + 4 * nb + (l32 & 3);
+      for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int mm = 0; mm < C::MB; ++mm)
+        for (int r = 0; r < 16; ++r) {
+          const int x = 8 * (r >> 2) + 4 * h + (r & 3);
+          const int qin = 32 * (x >> 4) + 8 * ((x >> 2) & 3) + 4 * nb + (x & 3);
 #pragma unroll
-          for (int g = 0; g < 4; ++g)
-            *(f32x4*)(dQg + (size_t)qin * rs + 32 * mm + 8 * g) =
-                f32x4{acc[mm][nb][4 * g], acc[mm][nb][4 * g + 1], acc[mm][nb][4 * g + 2], acc[mm][nb][4 * g + 3]} * kDsUnit;
-      }
+          for (int mm = 0; mm < C::MB; ++mm) dQg[(size_t)qin * rs + 32 * mm] = acc[mm][nb][r] * kDsUnit;
+        }
       s1 = true;
     }
 #pragma unroll
