@@ -29,7 +29,10 @@
 // second half's products run, and dS of the second half while the first dQ products run.
 // Scheduling fences keep that order. K and V tiles go global -> LDS by
 // global_load_lds_dwordx4 (no registers, untracked by the compiler), two stages: tile j+1 is
-// copied while tile j is used.
+// copied while tile j is used. At the end each wave reads its 32 rows of the old dQ with
+// 16-byte loads, all issued before the accumulators are transposed through LDS, and writes
+// old + sum back with 16-byte stores (element-wise loads, a few in flight at a time, took a
+// sixth of the kernel at T = 4096 and half of it at T = 1024).
 //
 // Matrix-core passes: S and dP sum d in passes of 8 consecutive values; dQ sums keys in passes
 // {16c+0..3, 16c+8..11} then {16c+4..7, 16c+12..15}.
@@ -162,21 +165,6 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   const int g16 = lane >> 4, s16 = lane & 15;
   const uint32_t tr_rd = 2 * ((4 * h + (s16 >> 2)) * C::P + 16 * (g16 & 1) + 4 * (s16 & 3));
 
-  // Matrix-core instruction i of a tile (compile-time after unrolling):
-  //   [0, KC): S of keys 0-31, d step i      [KC, 2KC): dP of keys 0-31
-  //   [2KC, 3KC): S of keys 32-63            [3KC, 4KC): dP of keys 32-63
-  //   [4KC, NM): dQ, key step c = k / DT, d tile dt = k % DT (k = i - 4KC)
-  auto operand = [&](int i, uint32_t kb, uint32_t vb) -> u32x4 {
-    if (i < 4 * C::KC) {
-      const int half = i / (2 * C::KC), isdp = (i / C::KC) & 1, c = i % C::KC;
-      return lds_b128_at((isdp ? vb : kb) + row_rd + 2 * (32 * half * C::P + 16 * c));
-    }
-    const int k = i - 4 * C::KC, dt = k % C::DT, c = k / C::DT;
-    const u32x2 lo = lds_tr_at(kb + tr_rd + 2 * (16 * c * C::P + 32 * dt));
-    const u32x2 hi = lds_tr_at(kb + tr_rd + 2 * ((16 * c + 8) * C::P + 32 * dt));
-    return u32x4{lo[0], lo[1], hi[0], hi[1]};
-  };
-
   f32x16 dQa[C::DT];
 #pragma unroll
   for (int i = 0; i < C::DT; ++i) dQa[i] = zero16();
@@ -307,6 +295,18 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   }
 
   // ---- dQ += result: transpose through LDS ([q][d] fp32), then row-contiguous read-add-writes ----
+  // The wave's 32 rows of the old dQ are read first, as 16-byte chunks (chunk u = 64i + lane is
+  // row u / (D/4), columns 4(u % (D/4)) .. +3), so the loads are in flight during the transpose.
+  constexpr int NCH = 32 * D / 4 / 64;  // 16-byte chunks per lane
+  float* dQg = a.dQ + base + (size_t)qw * rs;
+  f32x4 old[NCH];
+  if (wave_active) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int u = 64 * i + lane, r = u / (D / 4), c4 = u % (D / 4);
+      old[i] = *(const f32x4*)(dQg + (size_t)r * rs + 4 * c4);
+    }
+  }
   float* buf = (float*)smem + wave * 32 * C::DQP;
   if (wave_active) {
 #pragma unroll
@@ -318,11 +318,11 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   }
   __syncthreads();
   if (!wave_active) return;
-  float* dQg = a.dQ + base + (size_t)qw * rs;
-#pragma unroll 4
-  for (int r = 0; r < 32; ++r)
 #pragma unroll
-    for (int c = 0; c < D / 64; ++c) dQg[(size_t)r * rs + 64 * c + lane] += buf[r * C::DQP + 64 * c + lane];
+  for (int i = 0; i < NCH; ++i) {
+    const int u = 64 * i + lane, r = u / (D / 4), c4 = u % (D / 4);
+    *(f32x4*)(dQg + (size_t)r * rs + 4 * c4) = old[i] + *(const f32x4*)(buf + r * C::DQP + 4 * c4);
+  }
 }
 
 hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s) {
