@@ -420,6 +420,33 @@ def main():
             "avg_ms": round(kv_avg, 4),
         }
         roofline_dq = None
+    elif D == 64:
+        # the workspace entry point runs the recomputing kernels at D = 64 (no dS stored): dK/dV
+        # (4 products: S, dP, dV, dK) and dQ written (3 products: S, dP, dQ)
+        roofline = {
+            "kernel": "backward dK/dV kernel without the dS store (mla::bwd_kernel<64, false>; at D = 64 "
+                      "the workspace entry point recomputes dS instead of storing it)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": 12 * bthd + 8 * B * H * T,
+            "avg_ms": round(kv_avg, 4),
+        }
+        dq_exec = 3.0 * unit / (dq_avg * 1e-3) / 1e12
+        roofline_dq = {
+            "kernel": "backward dQ kernel recomputing S, dP and dS, dQ written (mla::bwd_dq_kernel<64, false>)",
+            "bound": "mfma",
+            "achieved": round(dq_exec, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dq_exec / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "note": "three executed products per launch (S, dP, dQ); one of them (dQ) is algorithmic",
+            "avg_ms": round(dq_avg, 4),
+        }
     else:
         roofline = {
             "kernel": "backward dK/dV kernel with the dS store (mla::bwd_kernel<D, true>)",

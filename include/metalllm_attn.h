@@ -111,9 +111,12 @@ int metalllmAttnBackwardWorkspaceSize(const AttentionParams* p, uint64_t* bytes)
  * what flashAttentionBackward adds into a zeroed dQ up to fp32 summation order. The workspace
  * holds no state between calls, but one
  * workspace must not serve two calls at once. Returns METALLLM_ATTN_E_NULL / _E_ALIGN / _E_SIZE
- * for a NULL, misaligned or too small workspace. For D = 64 and M <= 256 it runs the same single
- * kernel as flashAttentionBackward there (dS stays in LDS; the workspace is validated but not
- * used). No counterpart in the reference. */
+ * for a NULL, misaligned or too small workspace. At D = 64 no dS is stored and the workspace is
+ * validated but not used: for M <= 256 it runs the same single kernel as flashAttentionBackward
+ * there (dS stays in LDS); for longer sequences flashAttentionBackward's two kernels, the dQ kernel
+ * writing dQ instead of adding into it (at this head size the recomputation is faster than the dS
+ * round trip), so dQ, dK and dV equal flashAttentionBackward's into a zeroed dQ bit for bit.
+ * No counterpart in the reference. */
 int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                                     const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                                     void* workspace, uint64_t workspace_bytes, const AttentionParams* p,
@@ -124,12 +127,11 @@ int flashAttentionBackwardWorkspace(const uint16_t* dZ, const float* d, const fl
  * flashAttentionBackwardWorkspace (same kernels, bit-identical dQ, dK, dV; dQ written in full),
  * with the dS tiles in a fixed per-device array of METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64 MiB,
  * held by every GPU the library runs on until the process ends) instead of a caller workspace.
- * Calls no hipMalloc/hipFree. Shapes whose metalllmAttnBackwardWorkspaceSize exceeds the array
- * return METALLLM_ATTN_E_SIZE (e.g. B = 16, NH = 12, M = 512, D = 64 needs 56.6 MB and fits),
- * except D = 64 with M <= 256 (the reference's own shape, config 1 included), which runs the fused
- * short-sequence backward, stores no dS tiles and accepts any batch. All calls on one GPU share
- * the array: calls that overlap on one GPU race. The first call on a device looks up the array's
- * address there. */
+ * Calls no hipMalloc/hipFree. D = 128 shapes whose metalllmAttnBackwardWorkspaceSize exceeds the
+ * array return METALLLM_ATTN_E_SIZE (e.g. B = 4, NH = 12, M = 1024 needs 53.5 MB and fits; B = 8
+ * does not). D = 64 stores no dS tiles (see flashAttentionBackwardWorkspace) and accepts every
+ * shape. All calls on one GPU share the array: calls that overlap on one GPU race. The first call
+ * on a device looks up the array's address there. */
 #define METALLLM_ATTN_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                                   const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
@@ -304,7 +306,8 @@ int metalllmSublayerGraphDestroy(metalllmSublayerGraph* g);
  * then part 3). Timing the parts separately measures the same work. Same validation and return
  * codes as those entry points (parts 0 and 1 ignore the workspace arguments); a part outside
  * 0..3 returns METALLLM_ATTN_E_LAYOUT. For D = 64 and M <= 256 parts 0 and 2 launch the single
- * fused kernel (part 0 adds dQ, part 2 writes it) and parts 1 and 3 launch nothing. */
+ * fused kernel (part 0 adds dQ, part 2 writes it) and parts 1 and 3 launch nothing. For D = 64 and
+ * longer sequences parts 2 and 3 launch parts 0's and 1's kernels, part 3 writing dQ. */
 int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const float* l, const uint16_t* q,
                              const uint16_t* k, const uint16_t* v, float* dQ, uint16_t* dK, uint16_t* dV,
                              void* workspace, uint64_t workspace_bytes, const AttentionParams* p,

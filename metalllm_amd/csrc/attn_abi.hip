@@ -80,9 +80,18 @@ int metalllmAttnBackwardPart(int part, const uint16_t* dZ, const float* d, const
     return mla::launch_backward_short(a, part == 0, (hipStream_t)stream) == hipSuccess ? METALLLM_ATTN_OK
                                                                                          : METALLLM_ATTN_E_LAUNCH;
   }
-  const hipError_t e = part == 0 || part == 2 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
-                       : part == 1           ? mla::launch_backward_dq(a, (int)p->D, (hipStream_t)stream)
-                                             : mla::launch_backward_dqs(a, (int)p->D, (hipStream_t)stream);
+  hipError_t e;
+  if (part >= 2 && mla::workspace_recomputes(a.T, (int)p->D)) {
+    // the recomputing kernels, dQ written: faster than the dS round trip at this head size (the
+    // workspace is validated but not used)
+    a.dS = nullptr;
+    e = part == 2 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
+                  : mla::launch_backward_dq(a, (int)p->D, false, (hipStream_t)stream);
+  } else {
+    e = part == 0 || part == 2 ? mla::launch_backward(a, (int)p->D, (hipStream_t)stream)
+        : part == 1           ? mla::launch_backward_dq(a, (int)p->D, true, (hipStream_t)stream)
+                              : mla::launch_backward_dqs(a, (int)p->D, (hipStream_t)stream);
+  }
   return e == hipSuccess ? METALLLM_ATTN_OK : METALLLM_ATTN_E_LAUNCH;
 }
 

@@ -96,7 +96,8 @@ struct BoolTag {
   static constexpr bool value = V;
 };
 
-template <int D>
+// ACC: add the result into dQ (flashAttentionBackward's contract); otherwise write dQ.
+template <int D, bool ACC>
 __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   using C = DqCfg<D>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * C::STAGE];
@@ -300,7 +301,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   constexpr int NCH = 32 * D / 4 / 64;  // 16-byte chunks per lane
   float* dQg = a.dQ + base + (size_t)qw * rs;
   f32x4 old[NCH];
-  if (wave_active) {
+  if (ACC && wave_active) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int u = 64 * i + lane, r = u / (D / 4), c4 = u % (D / 4);
@@ -321,17 +322,25 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int u = 64 * i + lane, r = u / (D / 4), c4 = u % (D / 4);
-    *(f32x4*)(dQg + (size_t)r * rs + 4 * c4) = old[i] + *(const f32x4*)(buf + r * C::DQP + 4 * c4);
+    const f32x4 sum = *(const f32x4*)(buf + r * C::DQP + 4 * c4);
+    *(f32x4*)(dQg + (size_t)r * rs + 4 * c4) = ACC ? old[i] + sum : sum;
   }
 }
 
-hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s) {
+hipError_t launch_backward_dq(const BwdArgs& a, int D, bool accumulate, hipStream_t s) {
   const int nqb = (a.T + kDqBlockM - 1) / kDqBlockM;
   const dim3 grid((unsigned)(a.B * a.H * nqb));
-  if (D == 64)
-    hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(256), 0, s, a);
+  if (D == 64) {
+    if (accumulate)
+      hipLaunchKernelGGL((bwd_dq_kernel<64, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_dq_kernel<64, false>), grid, dim3(256), 0, s, a);
+  } else {
+    if (accumulate)
+      hipLaunchKernelGGL((bwd_dq_kernel<128, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_dq_kernel<128, false>), grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

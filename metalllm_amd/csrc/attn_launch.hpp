@@ -52,11 +52,18 @@ hipError_t launch_forward(const FwdArgs& a, int D, hipStream_t s);
 void forward_prepare();  // device queries of launch_forward, done ahead of a stream capture
 hipError_t launch_compute_d(const ComputeDArgs& a, int D, hipStream_t s);
 hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s);     // dK, dV (key-owner)
-hipError_t launch_backward_dq(const BwdArgs& a, int D, hipStream_t s);  // dQ (query-owner)
+// dQ (query-owner, recomputing dS): added into dQ (accumulate) or written
+hipError_t launch_backward_dq(const BwdArgs& a, int D, bool accumulate, hipStream_t s);
 hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s); // dQ from the stored dS
 // Short sequences (D = 64, T <= 256): dK, dV and dQ of a (b,h) pair by one workgroup, one launch,
 // no workspace; dQ added into (accumulate) or written.
 bool backward_is_short(int T, int D);
+// The workspace entry point runs the recomputing kernels (dK/dV without the dS store, then dQ
+// written) instead of the dS round trip: at D = 64 the dK/dV kernel without the store runs three
+// workgroups per CU and the pair is faster (config 2 step 0.436 -> 0.41 ms, config 4's 0.733 ->
+// 0.716 ms); at D = 128 the round trip saves two of seven products. T <= 256 at D = 64 runs the
+// fused short backward instead (backward_is_short).
+inline bool workspace_recomputes(int T, int D) { return D == 64 && T > 256; }
 hipError_t launch_backward_short(const BwdArgs& a, bool accumulate, hipStream_t s);
 
 // Dispatch chunk sizes, in workgroups per XCD group. The backward's is one round of resident

@@ -2,7 +2,8 @@
 // (flashAttentionBackwardWorkspace) for callers that cannot allocate device memory (code under
 // HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The dS tiles go into a
 // file-scope device array of METALLLM_ATTN_NOALLOC_SCRATCH_BYTES instead of a caller workspace;
-// shapes whose tiles do not fit are rejected. Every GPU the library runs on holds its own copy of
+// shapes whose tiles do not fit are rejected. At D = 64 the workspace entry point stores no dS
+// tiles (the fused short-sequence kernel, or the recomputing kernels), so every D = 64 shape fits. Every GPU the library runs on holds its own copy of
 // the array until the process ends, and every call on one GPU shares it: calls that overlap on one
 // GPU (different streams, or different host threads) race. The kernels write every dS tile they
 // read within one call, so the array needs no clearing between calls.
@@ -47,11 +48,11 @@ extern "C" int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d,
   uint64_t need = 0;
   const int rc = metalllmAttnBackwardWorkspaceSize(p, &need);  // validates the shape
   if (rc) return rc;
-  // D = 64, M <= 256 runs the fused short-sequence backward, which keeps dS in LDS and never
-  // reads the workspace: any batch size fits there, and the nominal size is passed on so that the
-  // workspace entry point's own size check accepts it
-  const bool short_path = mla::backward_is_short((int)p->M, (int)p->D);
-  if (!short_path && need > kScratchBytes) return METALLLM_ATTN_E_SIZE;
+  // At D = 64 the workspace entry point never reads the workspace (M <= 256: the fused
+  // short-sequence backward keeps dS in LDS; longer: the recomputing kernels): any shape fits
+  // there, and the nominal size is passed on so that the entry point's own size check accepts it
+  const bool no_tiles = mla::backward_is_short((int)p->M, (int)p->D) || mla::workspace_recomputes((int)p->M, (int)p->D);
+  if (!no_tiles && need > kScratchBytes) return METALLLM_ATTN_E_SIZE;
   if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
   if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
@@ -59,6 +60,6 @@ extern "C" int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d,
   void* ws = nullptr;
   const int src = scratch_on_current_device(&ws);
   if (src) return src;
-  return flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, ws, short_path ? need : kScratchBytes, p,
+  return flashAttentionBackwardWorkspace(dZ, d, l, q, k, v, dQ, dK, dV, ws, no_tiles ? need : kScratchBytes, p,
                                          stream);
 }

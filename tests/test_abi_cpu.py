@@ -111,24 +111,26 @@ def test_error_strings():
 
 
 def test_no_alloc_backward_validates_before_device():
-    """flashAttentionBackwardNoAlloc rejects shapes whose dS tiles exceed its fixed array (except
-    the fused short-sequence shapes, which store no tiles), bad shapes, NULL and misaligned pointers
-    before touching the device."""
+    """flashAttentionBackwardNoAlloc rejects shapes whose dS tiles exceed its fixed array (at
+    D = 128; at D = 64 the workspace entry point stores no tiles), bad shapes, NULL and misaligned
+    pointers before touching the device."""
     lib = M.library()
     f = lib.flashAttentionBackwardNoAlloc
     ok = ctypes.c_void_p(1 << 20)
-    fits = AttentionParams.of(16, 512, 12, 64)      # 56.6 MB of dS tiles
-    too_big = AttentionParams.of(32, 1024, 12, 64)  # config 2: 792 MiB
+    fits = AttentionParams.of(4, 1024, 12, 128)     # 53.5 MB of dS tiles
+    too_big = AttentionParams.of(8, 1024, 12, 128)  # 107 MB
+    assert M.workspace_bytes(4, 1024, 12, 128) <= M.attention.NOALLOC_SCRATCH_BYTES < M.workspace_bytes(8, 1024, 12, 128)
     assert f(*([ok] * 9), ctypes.byref(too_big), None) == -5
-    # D = 64, T <= 256 runs the fused short backward, which uses no workspace: config 1 (60 MiB of
-    # nominal tiles) and a batch 8x larger (480 MiB) pass the size step and stop at the NULL pointer
-    for short in (AttentionParams.of(128, 256, 6, 64), AttentionParams.of(1024, 256, 6, 64)):
-        assert f(*([ok] * 8), None, ctypes.byref(short), None) == -1
-    assert M.workspace_bytes(1024, 256, 6, 64) > M.attention.NOALLOC_SCRATCH_BYTES
+    # D = 64 stores no dS tiles: config 1 (60 MiB of nominal tiles, the fused short backward), a
+    # batch 8x larger (480 MiB), config 2 (792 MiB) and config 4's attention (T = 2048, 816 MiB; the
+    # recomputing kernels) pass the size step and stop at the NULL pointer
+    over = ((1024, 256, 6, 64), (32, 1024, 12, 64), (8, 2048, 12, 64))
+    assert all(M.workspace_bytes(*shape) > M.attention.NOALLOC_SCRATCH_BYTES for shape in over)
+    for shape in ((128, 256, 6, 64),) + over:
+        assert f(*([ok] * 8), None, ctypes.byref(AttentionParams.of(*shape)), None) == -1
     assert f(*([ok] * 9), ctypes.byref(AttentionParams.of(1, 100, 1, 64)), None) == -2
     assert f(*([ok] * 8), None, ctypes.byref(fits), None) == -1
     assert f(*([ok] * 8), ctypes.c_void_p((1 << 20) + 2), ctypes.byref(fits), None) == -6
-    assert M.workspace_bytes(16, 512, 12, 64) <= M.attention.NOALLOC_SCRATCH_BYTES < M.workspace_bytes(32, 1024, 12, 64)
 
 
 def test_sublayer_reserve_validates_before_device():

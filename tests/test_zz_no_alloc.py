@@ -38,17 +38,18 @@ def _run(gpu, B, T, H, D, seed):
 
 
 def test_no_alloc_backward_matches_workspace_backward(gpu):
-    # 56.6 MB of dS tiles, near the 64 MiB array (T = 512: the stored-dS kernels, not the fused
-    # short-sequence backward of T <= 256), then a smaller D = 128 input
-    _run(gpu, 16, 512, 12, 64, 61)
+    # D = 128 stores dS tiles in the array: 53.5 MB of them (near its 64 MiB), then a smaller input
+    _run(gpu, 4, 1024, 12, 128, 61)
     _run(gpu, 2, 512, 4, 128, 62)
-    # D = 64, T = 256 runs the fused short backward (dS in LDS, the array unused): accepted beyond
-    # the array's nominal size (120 MiB of tiles here)
+    # D = 64 stores no tiles (T <= 256: the fused short backward; longer: the recomputing kernels):
+    # accepted beyond the array's nominal size (120 MiB and 104 MiB of tiles here)
     _run(gpu, 256, 256, 6, 64, 63)
+    _run(gpu, 8, 2048, 3, 64, 64)
     import metalllm_amd as M
-    with pytest.raises(M.AttentionError):  # tiles beyond the array: rejected before the device
+    assert M.workspace_bytes(8, 2048, 3, 64) > M.attention.NOALLOC_SCRATCH_BYTES
+    with pytest.raises(M.AttentionError):  # D = 128 tiles beyond the array: rejected before the device
         import torch
-        x = torch.empty((32, 1024, 12, 64), dtype=torch.bfloat16, device=gpu)
-        d = torch.empty((32, 12, 1024), dtype=torch.float32, device=gpu)
-        dq = torch.empty((32, 1024, 12, 64), dtype=torch.float32, device=gpu)
+        x = torch.empty((8, 1024, 12, 128), dtype=torch.bfloat16, device=gpu)
+        d = torch.empty((8, 12, 1024), dtype=torch.float32, device=gpu)
+        dq = torch.empty((8, 1024, 12, 128), dtype=torch.float32, device=gpu)
         M.flashAttentionBackwardNoAlloc(x, d, d, x, x, x, dq, x, x)
