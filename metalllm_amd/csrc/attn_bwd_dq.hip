@@ -10,10 +10,11 @@
 // its 128 query rows over all keys, keeps dQ in matrix-core accumulators, and adds its sum to its
 // rows of dQ with one read-add-write per element (the only writer of those rows, so no atomics:
 // the device executes about 0.33e12 fp32 atomic adds per second, and the owner-side form, one
-// atomic per element per key tile, would cost more than the whole kernel at long sequences). dQ
-// keeps the reference's contract: the result is added to what the caller's buffer holds. The dQ product sums each query's keys in fp32 across key tiles (the
-// reference rounds each 64-key part to bf16 first, :288; the difference is far inside the
-// gradient tolerance).
+// atomic per element per key tile, would cost more than the whole kernel at long sequences). For
+// flashAttentionBackward dQ keeps the reference's contract: the result is added to what the
+// caller's buffer holds. The workspace entry point at D = 64 runs this kernel writing dQ instead.
+// The dQ product sums each query's keys in fp32 across key tiles (the reference rounds each
+// 64-key part to bf16 first, :288; the difference is far inside the gradient tolerance).
 //
 // Work split: 4 waves x 32 query rows per workgroup, two workgroups per CU (two waves per SIMD
 // hide each other's LDS and barrier waits). Lane = query: the wave computes S^T and dP^T
@@ -295,7 +296,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
     __syncthreads();
   }
 
-  // ---- dQ += result: transpose through LDS ([q][d] fp32), then row-contiguous read-add-writes ----
+  // ---- dQ += result (ACC) or dQ = result: transpose through LDS ([q][d] fp32), then row-contiguous writes ----
   // The wave's 32 rows of the old dQ are read first, as 16-byte chunks (chunk u = 64i + lane is
   // row u / (D/4), columns 4(u % (D/4)) .. +3), so the loads are in flight during the transpose.
   constexpr int NCH = 32 * D / 4 / 64;  // 16-byte chunks per lane
