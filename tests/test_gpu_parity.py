@@ -58,6 +58,8 @@ def check_case(gpu, B, T, H, D, s, seed, b_end=0, threads=0):
     (q0, k0, v0), (q1, k1, v1) = res
     assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
     assert np.abs(q0 - q1).max() <= 1e-5 * np.abs(q0).max()
+    if D == 64:  # the workspace entry point stores no dS there: the same kernels, dQ written
+        assert np.array_equal(q0, q1)
     return out, lse
 
 
