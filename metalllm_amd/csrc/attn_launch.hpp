@@ -58,11 +58,11 @@ hipError_t launch_backward_dqs(const BwdArgs& a, int D, hipStream_t s); // dQ fr
 // Short sequences (D = 64, T <= 256): dK, dV and dQ of a (b,h) pair by one workgroup, one launch,
 // no workspace; dQ added into (accumulate) or written.
 bool backward_is_short(int T, int D);
-// The workspace entry point runs the recomputing kernels (dK/dV without the dS store, then dQ
-// written) instead of the dS round trip: at D = 64 the dK/dV kernel without the store runs three
-// workgroups per CU and the pair is faster (config 2 step 0.436 -> 0.41 ms, config 4's 0.733 ->
-// 0.716 ms); at D = 128 the round trip saves two of seven products. T <= 256 at D = 64 runs the
-// fused short backward instead (backward_is_short).
+// Whether the workspace entry point runs the recomputing kernels (dK/dV without the dS store, then
+// dQ written) instead of the dS round trip. Yes at D = 64: the dK/dV kernel without the store runs
+// three workgroups per CU and the pair is faster (config 2 step 0.436 -> 0.41 ms, config 4's
+// 0.733 -> 0.716 ms); T <= 256 runs the fused short backward instead (backward_is_short). No at
+// D = 128, where the round trip saves two of the seven products.
 inline bool workspace_recomputes(int T, int D) { return D == 64 && T > 256; }
 hipError_t launch_backward_short(const BwdArgs& a, bool accumulate, hipStream_t s);
 

@@ -3,10 +3,11 @@
 // HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The dS tiles go into a
 // file-scope device array of METALLLM_ATTN_NOALLOC_SCRATCH_BYTES instead of a caller workspace;
 // shapes whose tiles do not fit are rejected. At D = 64 the workspace entry point stores no dS
-// tiles (the fused short-sequence kernel, or the recomputing kernels), so every D = 64 shape fits. Every GPU the library runs on holds its own copy of
-// the array until the process ends, and every call on one GPU shares it: calls that overlap on one
-// GPU (different streams, or different host threads) race. The kernels write every dS tile they
-// read within one call, so the array needs no clearing between calls.
+// tiles (the fused short-sequence kernel, or the recomputing kernels), so every D = 64 shape
+// fits. Every GPU the library runs on holds its own copy of the array until the process ends, and
+// every call on one GPU shares it: calls that overlap on one GPU (different streams, or different
+// host threads) race. The kernels write every dS tile they read within one call, so the array
+// needs no clearing between calls.
 #include <mutex>
 
 #include "../../include/metalllm_attn.h"
@@ -51,7 +52,8 @@ extern "C" int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d,
   // At D = 64 the workspace entry point never reads the workspace (M <= 256: the fused
   // short-sequence backward keeps dS in LDS; longer: the recomputing kernels): any shape fits
   // there, and the nominal size is passed on so that the entry point's own size check accepts it
-  const bool no_tiles = mla::backward_is_short((int)p->M, (int)p->D) || mla::workspace_recomputes((int)p->M, (int)p->D);
+  const int M = (int)p->M, D = (int)p->D;
+  const bool no_tiles = mla::backward_is_short(M, D) || mla::workspace_recomputes(M, D);
   if (!no_tiles && need > kScratchBytes) return METALLLM_ATTN_E_SIZE;
   if (!dZ || !d || !l || !q || !k || !v || !dQ || !dK || !dV) return METALLLM_ATTN_E_NULL;
   if (!aligned16(dZ) || !aligned16(d) || !aligned16(l) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
