@@ -141,7 +141,7 @@ int metalllmAttnWorkMap(int kind, const AttentionParams* p, int32_t* out, int32_
   const int grid = npairs * nblk;
   for (int i = 0; i < count && i < grid; ++i) {
     int pair, b;
-    const int round = kind == 0 ? mla::kFwdDispatchRound : mla::kBwdDispatchRound;
+    const int round = kind == 0 ? mla::kFwdDispatchRound : mla::bwd_dispatch_round((int)p->D);
     mla::decode_workgroup(i, npairs, nblk, kind != 1, round, pair, b);
     out[2 * i] = pair;
     out[2 * i + 1] = b;

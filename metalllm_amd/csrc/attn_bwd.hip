@@ -403,7 +403,7 @@ __global__ void __launch_bounds__(256, (D == 64 && !DS) ? 3 : 2) bwd_kernel(BwdA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (a.T + C::BN - 1) / C::BN;
   int pair, kb;
-  decode_workgroup(blockIdx.x, a.B * a.H, nkb, false, kBwdDispatchRound, pair, kb);
+  decode_workgroup(blockIdx.x, a.B * a.H, nkb, false, bwd_dispatch_round(D), pair, kb);
   const int b = pair / a.H, hd = pair - b * a.H;
   const int rs = a.H * D;
   const size_t base = ((size_t)b * a.T * a.H + hd) * D;
@@ -703,10 +703,9 @@ hipError_t launch_backward(const BwdArgs& a, int D, hipStream_t s) {
   const int nkb = (a.T + kBwdBlockN - 1) / kBwdBlockN;
   const dim3 grid((unsigned)(a.B * a.H * nkb));
   if (a.dS) {
-    if (D == 64)
-      hipLaunchKernelGGL((bwd_kernel<64, true>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((bwd_kernel<128, true>), grid, dim3(256), 0, s, a);
+    // at D = 64 the workspace entry point stores no dS (workspace_recomputes, backward_is_short)
+    if (D == 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((bwd_kernel<128, true>), grid, dim3(256), 0, s, a);
   } else {
     if (D == 64)
       hipLaunchKernelGGL((bwd_kernel<64, false>), grid, dim3(256), 0, s, a);

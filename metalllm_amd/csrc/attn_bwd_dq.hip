@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(256, 2) bwd_dq_kernel(BwdArgs a) {
   const int h = lane >> 5, l32 = lane & 31;
   const int nqb = (a.T + C::BM - 1) / C::BM;
   int pair, qb;
-  decode_workgroup(blockIdx.x, a.B * a.H, nqb, true, kBwdDispatchRound, pair, qb);
+  decode_workgroup(blockIdx.x, a.B * a.H, nqb, true, bwd_dispatch_round(D), pair, qb);
   const int b = pair / a.H, hd = pair - b * a.H;
   const int rs = a.H * D;
   const size_t base = ((size_t)b * a.T * a.H + hd) * D;

@@ -73,6 +73,13 @@ hipError_t launch_backward_short(const BwdArgs& a, bool accumulate, hipStream_t 
 // 2.39 and 2.37 ms.
 constexpr int kFwdDispatchRound = 128;
 constexpr int kBwdDispatchRound = 64;
+// At D = 64 the backward's kernels (dK/dV without the dS store, the recomputing dQ kernel) run
+// three workgroups per CU, 96 per XCD, and their chunks span two such rounds. Measured on one box
+// (the workspace backward at config 2 and at config 4's attention shape): chunks of 64, 96, 192
+// workgroups and all of an XCD's pairs in one chunk gave 0.317, 0.325, 0.306, 0.303 ms and 0.263,
+// 0.272, 0.240, 0.239 ms; with 64 the last chunk's long blocks started late and ran alone.
+constexpr int kBwdDispatchRound64 = 192;
+__host__ __device__ inline int bwd_dispatch_round(int D) { return D == 64 ? kBwdDispatchRound64 : kBwdDispatchRound; }
 
 // Pairs per dispatch chunk: enough that one chunk's blocks fill a round of resident workgroups.
 __host__ __device__ inline int dispatch_chunk(int nblk, int group_slots) {
@@ -83,7 +90,7 @@ __host__ __device__ inline int dispatch_chunk(int nblk, int group_slots) {
 // Workgroup -> (pair = b*H + h, block) decode shared by host tests and kernels. Pairs are
 // spread so that every block of one pair lands on the same XCD (workgroups are handed to the
 // 8 XCDs round-robin by id). A group's pairs are taken in chunks of dispatch_chunk(nblk, round)
-// pairs (round: workgroups per XCD group, kFwdDispatchRound or kBwdDispatchRound); inside
+// pairs (round: workgroups per XCD group, kFwdDispatchRound or bwd_dispatch_round(D)); inside
 // a chunk the blocks go out block-major, the largest causal work first, across the chunk's pairs:
 //   forward : block = query block, longest (last) first
 //   backward: block = key block, longest (first) first

@@ -31,11 +31,13 @@ def test_partition(B, T, H, D, kind, blk, last_first):
         for p in range(npairs):
             assert len(set((np.nonzero(wm[:, 0] == p)[0] % 8).tolist())) == 1
     # per dispatch group (an XCD's share when the pairs split over 8, else the whole grid): a chunk
-    # of C pairs, C * nblk >= 64 workgroups per XCD for the backward (one round of resident
-    # workgroups) and 128 for the forward, is dispatched with non-increasing work, and a chunk's
-    # pairs are consecutive in the group
+    # of C pairs, C * nblk >= 64 workgroups per XCD for the D = 128 backward (one round of resident
+    # workgroups, two per CU), 192 for the D = 64 backward (two rounds of three per CU) and 128 for
+    # the forward, is dispatched with non-increasing work, and a chunk's pairs are consecutive in
+    # the group
     groups = [np.arange(x, len(wm), 8) for x in range(8)] if npairs % 8 == 0 else [np.arange(len(wm))]
-    rnd = (128 if kind == 0 else 64) * (1 if npairs % 8 == 0 else 8)
+    rnd = (128 if kind == 0 else (192 if D == 64 else 64)) * (1 if npairs % 8 == 0 else 8)
+    per_xcd = 96 if (kind != 0 and D == 64) else 64  # resident workgroups per XCD
     C = max(1, -(-rnd // nblk))
     for ids in groups:
         w, pr = work[ids], wm[ids, 0]
@@ -46,7 +48,7 @@ def test_partition(B, T, H, D, kind, blk, last_first):
         # cost): no later than dispatching the same pairs one after another, each pair's blocks
         # longest first
         def makespan(ws):
-            slots = [0.0] * min(64 if npairs % 8 == 0 else 512, len(ws))
+            slots = [0.0] * min(per_xcd if npairs % 8 == 0 else 8 * per_xcd, len(ws))
             for d in ws:
                 heapq.heappush(slots, heapq.heappop(slots) + d + 1.0)
             return max(slots)
