@@ -41,6 +41,9 @@ bool grad_dw_fused_ok(int R, int C);
 size_t grad_dw_partial_floats(int R, int C);
 hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
                           uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, bool accumulate, hipStream_t s);
+size_t grad_dw_one_partial_floats(int R, int C);
+hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
+                              bool accumulate, hipStream_t s);
 }  // namespace mla
 
 namespace {
@@ -205,11 +208,12 @@ size_t split_need(int R, int C) {
   return mla::grad_dx_fused_ok(R, C) && mla::grad_dw_fused_ok(R, C) ? 0 : 2 * (size_t)R * C;
 }
 
-// fp32 partial floats for projBackwarddW (row_chunks(R) products of C x C) and computeGradDw (the
-// hand-written kernel's chunks, or twice row_chunks(R) for the library path).
+// fp32 partial floats for projBackwarddW and computeGradDw: the hand-written kernel's chunks, or
+// row_chunks(R) products of C x C (twice that for computeGradDw's dQw) on the library path.
 size_t partial_need(int R, int C) {
-  const size_t lib = (size_t)row_chunks(R) * C * C;
-  return mla::grad_dw_fused_ok(R, C) ? std::max(lib, mla::grad_dw_partial_floats(R, C)) : 2 * lib;
+  if (mla::grad_dw_fused_ok(R, C))
+    return std::max(mla::grad_dw_one_partial_floats(R, C), mla::grad_dw_partial_floats(R, C));
+  return 2 * (size_t)row_chunks(R) * C * C;
 }
 
 int xt_g_partials(const Ctx& c, const uint16_t* X, const uint16_t* G, int R, int C, int parts, float* out) {
@@ -279,10 +283,18 @@ int op_proj_fwd(const Ctx& c, const uint16_t* attn_out, const uint16_t* proj_w, 
   return gemm_rm(c, false, false, R, C, C, attn_out, BF, C, proj_w, BF, C, 0.0f, out, BF, C);
 }
 
-// partial: at least row_chunks(R) * C * C floats. accumulate = false: dProjw is written as if it
-// held zeros (the phase encoder; every op_* below takes the same flag).
+// partial: at least partial_need(R, C) floats. accumulate = false: dProjw is written as if it
+// held zeros (the phase encoder; every op_* below takes the same flag). Row counts that are
+// multiples of 128 and feature counts that are multiples of 128 run computeGradDw's hand-written
+// kernel (sublayer_gemm.hip) on the one bf16 gradient; other shapes use the library.
 int op_proj_dw(const Ctx& c, const uint16_t* attn_out, const uint16_t* dZ, uint16_t* dProjw, int R, int C,
                float* partial, bool accumulate = true) {
+  if (mla::grad_dw_fused_ok(R, C)) {
+    if (c.query) return METALLLM_ATTN_OK;
+    return mla::launch_grad_dw_one(attn_out, dZ, dProjw, partial, R, C, accumulate, c.stream) == hipSuccess
+               ? METALLLM_ATTN_OK
+               : METALLLM_ATTN_E_LAUNCH;
+  }
   const int parts = row_chunks(R);
   TRY(xt_g_partials(c, attn_out, dZ, R, C, parts, partial));
   return reduce_into(c, partial, parts, (size_t)C * C, dProjw, true, accumulate);

@@ -395,15 +395,16 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
 }
 
 // dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw = bf16(previous + the sum of
-// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread. Without
-// acc the destinations are written as if they held zeros (bit for bit 0 + sum), and not read.
+// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread. Only the
+// weights w0 .. w0 + nw - 1 (0 dQw, 1 dKw, 2 dVw) are reduced. Without acc the destinations are
+// written as if they held zeros (bit for bit 0 + sum), and not read.
 __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __restrict__ part, float* __restrict__ dQw,
                                                                uint16_t* __restrict__ dKw, uint16_t* __restrict__ dVw,
-                                                               int C, int nq, int nkv, bool acc_dst) {
+                                                               int C, int nq, int nkv, int w0, int nw, bool acc_dst) {
   const size_t cc = (size_t)C * C, n4 = cc / 4;
-  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < 3 * n4; e += (size_t)gridDim.x * blockDim.x) {
-    const int w = (int)(e / n4);
-    const size_t o = 4 * (e - (size_t)w * n4);
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < nw * n4; e += (size_t)gridDim.x * blockDim.x) {
+    const int w = w0 + (int)(e / n4);
+    const size_t o = 4 * (e - (size_t)(w - w0) * n4);
     const int p0 = w == 0 ? 0 : nq + (w - 1) * nkv, np = w == 0 ? nq : nkv;
     f32x4 acc = *(const f32x4*)(part + (size_t)p0 * cc + o);
     for (int p = 1; p < np; ++p) acc += *(const f32x4*)(part + (size_t)(p0 + p) * cc + o);
@@ -429,6 +430,21 @@ GwShape grad_dw_shape(int R, int C, int cus) {
   sh.nkv = std::max(1, std::min(2 * cus / (4 * tiles), sh.steps / 2));
   sh.nq = 2 * sh.nkv;
   sh.items = tiles * (sh.nq + 2 * sh.nkv);
+  sh.per_xcd = sh.items % 8 == 0 ? sh.items / 8 : 0;
+  return sh;
+}
+
+// One bf16 gradient (projBackwarddW): no dWq items, every item takes the dKw path with G = dZ; as
+// many row chunks as fill one round of two workgroups per CU.
+GwShape grad_dw_one_shape(int R, int C, int cus) {
+  GwShape sh;
+  sh.C = C;
+  sh.nt = C / kGwTile;
+  sh.steps = R / kGwK;
+  const int tiles = sh.nt * sh.nt;
+  sh.nq = 0;
+  sh.nkv = std::max(1, std::min(2 * cus / tiles, sh.steps / 2));
+  sh.items = tiles * sh.nkv;
   sh.per_xcd = sh.items % 8 == 0 ? sh.items / 8 : 0;
   return sh;
 }
@@ -462,7 +478,24 @@ hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK
   if (e != hipSuccess) return e;
   const size_t n4 = 3 * (size_t)C * C / 4;
   hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
-                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv, accumulate);
+                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv, 0, 3, accumulate);
+  return hipGetLastError();
+}
+
+size_t grad_dw_one_partial_floats(int R, int C) {
+  const GwShape sh = grad_dw_one_shape(R, C, device_cus());
+  return (size_t)sh.nkv * C * C;
+}
+
+hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
+                              bool accumulate, hipStream_t s) {
+  const GwShape sh = grad_dw_one_shape(R, C, device_cus());
+  hipLaunchKernelGGL(grad_dw_kernel, dim3((unsigned)sh.items), dim3(256), 0, s, X, nullptr, G, G, partial, sh);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n4 = (size_t)C * C / 4;
+  hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
+                     partial, nullptr, dW, nullptr, C, 0, sh.nkv, 1, 1, accumulate);
   return hipGetLastError();
 }
 
