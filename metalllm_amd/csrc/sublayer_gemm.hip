@@ -231,12 +231,18 @@ struct GwShape {
   int steps;        // R / kGwK
   int nq, nkv;      // row chunks of dWq, and of each of dKw and dVw
   int items;        // nt^2 (nq + 2 nkv)
-  int per_xcd;      // items / 8 when 8 divides items, else 0
+  // XCD deal (0 in lx: workgroup order): XCD x takes items long0 + x lx + k for k < lx, then
+  // short0 + x sx + (k - lx)
+  int lx, sx, long0, short0;
 };
 
-// Work items in order (weight, chunk, i block, j block): dWq's, then dKw's, then dVw's. Workgroups
-// are dealt to the 8 XCDs in turn (blockIdx % 8), so when 8 divides the item count each XCD takes
-// a contiguous range of items: the items that share a chunk's rows run on one XCD and share its L2.
+// Work items in order (weight, chunk, i block, j block): dWq's, then dKw's, then dVw's.
+// Workgroups are dealt to the 8 XCDs in turn (blockIdx % 8, workgroup k of an XCD is blockIdx / 8).
+// When 8 divides the item count of each kind, each XCD takes a contiguous range of the longer
+// kind's items first (the kind with more products per item: dWq's or dKw's and dVw's), then a
+// contiguous range of the other kind's: the items that share a chunk's rows run on one XCD and
+// share its L2, and an XCD's first workgroups, which start one on each CU, carry the long items,
+// so that a CU's second workgroup is a short one.
 __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
                                                         float* __restrict__ part, GwShape sh) {
@@ -245,7 +251,11 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31, g16 = lane >> 4, s16 = lane & 15;
   const int C = sh.C, tiles = sh.nt * sh.nt;
-  int item = sh.per_xcd ? (int)(blockIdx.x % 8) * sh.per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  int item = (int)blockIdx.x;
+  if (sh.lx) {
+    const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
+    item = k < sh.lx ? sh.long0 + x * sh.lx + k : sh.short0 + x * sh.sx + (k - sh.lx);
+  }
   int wsel = 0, nch = sh.nq, pbase = 0;
   if (item >= tiles * sh.nq) {
     item -= tiles * sh.nq;
@@ -420,17 +430,31 @@ __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __rest
   }
 }
 
+// The XCD deal of GwShape for nq_items dWq items (first in item order) and kv_items dKw and dVw
+// items; q_long: dWq's items carry more products than the others'.
+void deal(GwShape& sh, int nq_items, int kv_items, bool q_long) {
+  sh.lx = sh.sx = sh.long0 = sh.short0 = 0;
+  if (nq_items % 8 || kv_items % 8) return;
+  sh.lx = (q_long ? nq_items : kv_items) / 8;
+  sh.sx = (q_long ? kv_items : nq_items) / 8;
+  sh.long0 = q_long ? 0 : nq_items;
+  sh.short0 = q_long ? nq_items : 0;
+}
+
 GwShape grad_dw_shape(int R, int C, int cus) {
   GwShape sh;
   sh.C = C;
   sh.nt = C / kGwTile;
   sh.steps = R / kGwK;
   const int tiles = sh.nt * sh.nt;
-  // one round of items on two workgroups per CU; dWq chunks are twice as many (half as long)
-  sh.nkv = std::max(1, std::min(2 * cus / (4 * tiles), sh.steps / 2));
-  sh.nq = 2 * sh.nkv;
+  // as many items per tile as fill one round of two workgroups per CU (k), split so that a dWq
+  // item (2 steps / nq products per row step) and a dKw or dVw item (steps / nkv) are as close as
+  // k allows: 6 and 4 chunks at C = 768 on 256 CUs (504 items, 85 and 64 product-steps)
+  const int k = std::max(4, 2 * cus / tiles);
+  sh.nkv = std::max(1, std::min((k + 2) / 4, sh.steps / 2));
+  sh.nq = std::max(1, std::min(k - 2 * sh.nkv, sh.steps));
   sh.items = tiles * (sh.nq + 2 * sh.nkv);
-  sh.per_xcd = sh.items % 8 == 0 ? sh.items / 8 : 0;
+  deal(sh, tiles * sh.nq, 2 * tiles * sh.nkv, 2 * sh.nkv > sh.nq);
   return sh;
 }
 
@@ -445,7 +469,7 @@ GwShape grad_dw_one_shape(int R, int C, int cus) {
   sh.nq = 0;
   sh.nkv = std::max(1, std::min(2 * cus / tiles, sh.steps / 2));
   sh.items = tiles * sh.nkv;
-  sh.per_xcd = sh.items % 8 == 0 ? sh.items / 8 : 0;
+  deal(sh, 0, sh.items, false);
   return sh;
 }
 

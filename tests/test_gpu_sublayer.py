@@ -66,9 +66,10 @@ def test_forward_gemms(gpu, S):
 def test_backward_gemms(gpu, S, B, T, H, C):
     """R and C multiples of 128 run the hand-written computeGradDx and computeGradDw kernels (fp32
     dQ split in registers); the last shape runs the library path on the split dQ. For
-    computeGradDw, R=512, C=768 gives 432 work items (dealt to the XCDs in contiguous ranges) and
-    R=384, C=384 gives 108 (not a multiple of 8: workgroup order) with dWq chunks of one 64-row
-    step; both are called twice, so the second call accumulates into nonzero destinations."""
+    computeGradDw, R=512, C=768 gives 504 work items (6 dWq and 4 dKw/dVw row chunks per tile,
+    the long dWq items dealt to each XCD first) and R=384, C=384 gives 108 (not a multiple of 8:
+    workgroup order) with dWq chunks of one 64-row step; projBackwarddW takes 144 and 27 one-weight
+    items. All are called twice, so the second call accumulates into nonzero destinations."""
     import torch
     R = B * T
     X, (Wq, Wk, Wv, Wp) = inputs(R, C, 2)
