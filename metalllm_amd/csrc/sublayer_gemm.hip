@@ -13,12 +13,12 @@
 //
 // computeGradDx: all three products accumulate into one set of fp32 accumulators, so dX is read
 // and written once instead of once per product. Tiling: a workgroup of 4 waves computes a 128
-// (rows r) x 128 (features i) tile of dX as
+// (rows r) x FI (features i, FI = 128 or 192) tile of dX as
 // dX^T = W . G^T (m = i, n = r, k = j): the A operand is a weight row W[i][j..j+7] and the B
 // operand a gradient row G[r][j..j+7], both 16-byte reads from row-major LDS tiles (pitch 72
 // elements: conflict-free 16-byte row reads), and each lane ends with four consecutive i of one
-// row r, stored as 16-byte words. Wave w owns the 64 x 64 quarter (i block w%2, r block w/2) as
-// 2 x 2 tiles of v_mfma_f32_32x32x16_bf16. The k loop runs over 64-wide steps of j: C/64 steps
+// row r, stored as 16-byte words. Wave w owns the FI/2 x 64 part (i block w%2, r block w/2) as
+// FI/64 x 2 tiles of v_mfma_f32_32x32x16_bf16. The k loop runs over 64-wide steps of j: C/64 steps
 // of dQ (hi and lo products share the weight operand), then of dK, then of dV. Each step's tiles
 // are loaded into registers during the previous step's products and written to LDS (dQ split on
 // the way) between two barriers.
@@ -34,7 +34,7 @@ namespace mla {
 
 namespace {
 
-constexpr int kGxTile = 128;        // rows and features per workgroup
+constexpr int kGxTile = 128;        // rows per workgroup (and the smaller feature tile)
 constexpr int kGxK = 64;            // j per step
 constexpr int kGxP = kGxK + 8;      // LDS row pitch (elements)
 constexpr int kGxTileBytes = kGxTile * kGxP * 2;
@@ -45,34 +45,38 @@ __device__ __forceinline__ void lds_st8(uint32_t a, u32x2 v) { *(__attribute__((
 
 // ACC: dX += the products (the reference's contract); otherwise dX = 0 + the products, written
 // without reading dX (the phase encoder, which would zero dX just before).
-template <bool ACC>
+template <bool ACC, int FI>
 __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
                                                         const uint16_t* __restrict__ Wq, const uint16_t* __restrict__ Wk,
                                                         const uint16_t* __restrict__ Wv, int C, int items) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[3 * kGxTileBytes];  // W, G hi, G lo
+  static_assert(FI == 128 || FI == 192, "feature tile");
+  constexpr int MI = FI / 64;                          // 32-wide i tiles per wave
+  constexpr int WQ = FI / 32;                          // W tile chunks per thread
+  constexpr int WBYTES = FI * kGxP * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[WBYTES + 2 * kGxTileBytes];  // W, G hi, G lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   // tile order: row block major, feature block minor. Workgroups are dealt to the 8 XCDs in turn
   // (blockIdx % 8); when 8 divides the tile count each XCD takes a contiguous range of tiles, so
-  // the C/128 tiles that read the same gradient rows run together on one XCD and share its L2.
-  const int nfb = C / kGxTile;
+  // the C/FI tiles that read the same gradient rows run together on one XCD and share its L2.
+  const int nfb = C / FI;
   const int item = items % 8 == 0 ? (int)(blockIdx.x % 8) * (items / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
-  const int r0 = (item / nfb) * kGxTile, i0 = (item % nfb) * kGxTile;
+  const int r0 = (item / nfb) * kGxTile, i0 = (item % nfb) * FI;
   const int wi = wave & 1, wr = wave >> 1;
   const uint32_t sW = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
-  const uint32_t sH = sW + kGxTileBytes, sL = sW + 2 * kGxTileBytes;
+  const uint32_t sH = sW + WBYTES, sL = sH + kGxTileBytes;
   const int nb = C / kGxK;  // steps per segment
 
-  // Copy roles. bf16 tiles (128 rows x 64 j): thread t moves 16-byte chunks c = t + 256q, q < 4
-  // (row c/8, chunk c%8). The fp32 dQ tile: chunks c = t + 256q, q < 8, of 4 floats (row c/16,
-  // floats 4(c%16)..+3), split and written as 8-byte hi and lo words.
-  u32x4 wreg[4], greg[4];
+  // Copy roles. bf16 tiles (128 or FI rows x 64 j): thread t moves 16-byte chunks c = t + 256q,
+  // q < 4 (W: q < FI/32) (row c/8, chunk c%8). The fp32 dQ tile: chunks c = t + 256q, q < 8, of
+  // 4 floats (row c/16, floats 4(c%16)..+3), split and written as 8-byte hi and lo words.
+  u32x4 wreg[WQ], greg[4];
   f32x4 qreg[8];
   auto load_w = [&](const uint16_t* W, int j0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < WQ; ++q) {
       const int c = tid + 256 * q, row = c >> 3, ch = c & 7;
       wreg[q] = *(const u32x4*)(W + (size_t)(i0 + row) * C + j0 + 8 * ch);
     }
@@ -93,7 +97,7 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
   };
   auto store_w = [&]() {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < WQ; ++q) {
       const int c = tid + 256 * q, row = c >> 3, ch = c & 7;
       lds_st16(sW + 2 * (row * kGxP + 8 * ch), wreg[q]);
     }
@@ -120,11 +124,11 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
   };
 
   // operand addresses: A = W row i (m), B = G row r (n); lane row l32, j = 16ks + 8h
-  const uint32_t aoff = 2 * ((64 * wi + l32) * kGxP + 8 * h);
+  const uint32_t aoff = 2 * ((FI / 2 * wi + l32) * kGxP + 8 * h);
   const uint32_t boff = 2 * ((64 * wr + l32) * kGxP + 8 * h);
-  f32x16 acc[2][2];
+  f32x16 acc[MI][2];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = zero16();
   // one 64-wide step of products from the staged tiles; TWO: dQ steps (hi and lo share A)
@@ -132,15 +136,16 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
     constexpr bool TWO = decltype(two_tag)::value;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      u32x4 A[2], Bh[2], Bl[2];
+      u32x4 A[MI], Bh[2], Bl[2];
+#pragma unroll
+      for (int t = 0; t < MI; ++t) A[t] = lds_ld16(sW + aoff + 2 * (32 * t * kGxP + 16 * ks));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        A[t] = lds_ld16(sW + aoff + 2 * (32 * t * kGxP + 16 * ks));
         Bh[t] = lds_ld16(sH + boff + 2 * (32 * t * kGxP + 16 * ks));
         if (TWO) Bl[t] = lds_ld16(sL + boff + 2 * (32 * t * kGxP + 16 * ks));
       }
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
           acc[mi][ni] = mfma(A[mi], Bh[ni], acc[mi][ni]);
@@ -185,13 +190,13 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
     }
   }
 
-  // dX^T tile (mi, ni): lane holds row r = r0 + 64wr + 32ni + l32, features i0 + 64wi + 32mi +
+  // dX^T tile (mi, ni): lane holds row r = r0 + 64wr + 32ni + l32, features i0 + (FI/2)wi + 32mi +
   // 8g + 4h + (0..3) in registers 4g..4g+3
 #pragma unroll
   for (int ni = 0; ni < 2; ++ni) {
-    float* row = dX + (size_t)(r0 + 64 * wr + 32 * ni + l32) * C + i0 + 64 * wi + 4 * h;
+    float* row = dX + (size_t)(r0 + 64 * wr + 32 * ni + l32) * C + i0 + FI / 2 * wi + 4 * h;
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         f32x4* p = (f32x4*)(row + 32 * mi + 8 * g);
@@ -523,13 +528,15 @@ hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW
   return hipGetLastError();
 }
 
+// Feature tile: 192 where it divides C (config 4's C = 768: 512 tiles of 128 x 192 fill one round
+// of two workgroups per CU, where 768 tiles of 128 x 128 took a round and a half), else 128.
 hipError_t launch_grad_dx(float* dX, const float* dQ, const uint16_t* dK, const uint16_t* dV, const uint16_t* Wq,
                           const uint16_t* Wk, const uint16_t* Wv, int R, int C, bool accumulate, hipStream_t s) {
-  const int items = (R / kGxTile) * (C / kGxTile);
-  if (accumulate)
-    hipLaunchKernelGGL(grad_dx_kernel<true>, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
-  else
-    hipLaunchKernelGGL(grad_dx_kernel<false>, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
+  const bool wide = C % 192 == 0;
+  const int items = (R / kGxTile) * (C / (wide ? 192 : 128));
+  auto kern = wide ? (accumulate ? grad_dx_kernel<true, 192> : grad_dx_kernel<false, 192>)
+                   : (accumulate ? grad_dx_kernel<true, 128> : grad_dx_kernel<false, 128>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)items), dim3(256), 0, s, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
   return hipGetLastError();
 }
 
