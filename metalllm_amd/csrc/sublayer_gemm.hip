@@ -222,9 +222,9 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
 // operands need 8 rows r of one column per lane: they come from row-major LDS tiles [r][128
 // columns] by ds_read_b64_tr_b16 (pitch 160 elements: the 4 rows x 64 bytes read by 32 lanes of
 // one transposing read fall in distinct banks).
-constexpr int kGwTile = 128;
+constexpr int kGwTile = 128;                     // output features j per tile (and the narrower i width)
 constexpr int kGwK = 64;                         // rows r per step
-constexpr int kGwP = kGwTile + 32;               // LDS row pitch (elements)
+constexpr int kGwP = kGwTile + 32;               // LDS row pitch of a 128-column tile (elements)
 constexpr int kGwTileBytes = kGwK * kGwP * 2;    // 20 KB
 
 __device__ __forceinline__ u32x2 lds_tr8(uint32_t a) {
@@ -232,7 +232,7 @@ __device__ __forceinline__ u32x2 lds_tr8(uint32_t a) {
 }
 
 struct GwShape {
-  int C, nt;        // features, tiles per side
+  int C, nti, ntj;  // features; tiles along i (FI wide) and along j (128 wide)
   int steps;        // R / kGwK
   int nq, nkv;      // row chunks of dWq, and of each of dKw and dVw
   int items;        // nt^2 (nq + 2 nkv)
@@ -248,14 +248,21 @@ struct GwShape {
 // contiguous range of the other kind's: the items that share a chunk's rows run on one XCD and
 // share its L2, and an XCD's first workgroups, which start one on each CU, carry the long items,
 // so that a CU's second workgroup is a short one.
+template <int FI>
 __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
                                                         float* __restrict__ part, GwShape sh) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[3 * kGwTileBytes];  // X, G (dQ hi), dQ lo
+  static_assert(FI == 128 || FI == 192, "input-feature tile");
+  constexpr int NI = FI / 64;                 // 32-wide i tiles per wave
+  constexpr int XQ = FI / 32;                 // X tile chunks per thread
+  constexpr int XCH = FI / 8;                 // 16-byte chunks per X row
+  constexpr int XP = FI + 32;                 // X tile pitch (elements)
+  constexpr int XBYTES = kGwK * XP * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[XBYTES + 2 * kGwTileBytes];  // X, G (dQ hi), dQ lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31, g16 = lane >> 4, s16 = lane & 15;
-  const int C = sh.C, tiles = sh.nt * sh.nt;
+  const int C = sh.C, tiles = sh.nti * sh.ntj;
   int item = (int)blockIdx.x;
   if (sh.lx) {
     const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
@@ -270,22 +277,23 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
     pbase = sh.nq + (wsel - 1) * sh.nkv;
   }
   const int chunk = item / tiles, tile = item - chunk * tiles;
-  const int i0 = (tile / sh.nt) * kGwTile, j0 = (tile % sh.nt) * kGwTile;
+  const int i0 = (tile / sh.ntj) * FI, j0 = (tile % sh.ntj) * kGwTile;
   const int s0 = (int)((long)chunk * sh.steps / nch), s1 = (int)((long)(chunk + 1) * sh.steps / nch);
   const uint16_t* G = wsel == 1 ? dK : dV;
   const int wi = wave & 1, wj = wave >> 1;
   const uint32_t sX = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
-  const uint32_t sH = sX + kGwTileBytes, sL = sX + 2 * kGwTileBytes;
+  const uint32_t sH = sX + XBYTES, sL = sH + kGwTileBytes;
 
-  // copies of a step's tiles (64 rows): bf16, c = t + 256q, q < 4: row c/16, 16-byte chunk c%16;
-  // fp32 dQ, c = t + 256q, q < 8: row c/32, floats 4(c%32)..+3
-  u32x4 xreg[4], greg[4];
+  // copies of a step's tiles (64 rows): bf16 G, c = t + 256q, q < 4: row c/16, 16-byte chunk c%16
+  // (X: q < FI/32, row c/(FI/8), chunk c%(FI/8)); fp32 dQ, c = t + 256q, q < 8: row c/32, floats
+  // 4(c%32)..+3
+  u32x4 xreg[XQ], greg[4];
   f32x4 qreg[8];
   auto load_x = [&](int r) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < XQ; ++q) {
       const int c = tid + 256 * q;
-      xreg[q] = *(const u32x4*)(X + (size_t)(r + (c >> 4)) * C + i0 + 8 * (c & 15));
+      xreg[q] = *(const u32x4*)(X + (size_t)(r + c / XCH) * C + i0 + 8 * (c % XCH));
     }
   };
   auto load_g = [&](int r) {
@@ -304,9 +312,9 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   };
   auto store_x = [&]() {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < XQ; ++q) {
       const int c = tid + 256 * q;
-      lds_st16(sX + 2 * ((c >> 4) * kGwP + 8 * (c & 15)), xreg[q]);
+      lds_st16(sX + 2 * ((c / XCH) * XP + 8 * (c % XCH)), xreg[q]);
     }
   };
   auto store_g = [&]() {
@@ -333,34 +341,39 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   // transposing reads of a 32-column block: source lane s16 of group g16 addresses row
   // 4h + s16/4 (+8 for the second read, +16 per k step), column 16(g16%2) + 4(s16%4); the lane
   // receives column l32 of the block at rows {4h..4h+3, 8+4h..8+4h+3}, the same rows for both
-  // operands
-  const uint32_t tr = 2 * ((4 * h + (s16 >> 2)) * kGwP + 16 * (g16 & 1) + 4 * (s16 & 3));
-  auto tr_op = [&](uint32_t base, int col0, int ks) -> u32x4 {
-    const uint32_t a = base + tr + 2 * (16 * ks * kGwP + col0);
-    const u32x2 lo = lds_tr8(a), hi = lds_tr8(a + 2 * 8 * kGwP);
+  // operands. Both pitches (160 and FI + 32 elements) put the 4 rows x 64 bytes that 32 lanes
+  // of one read touch in distinct banks.
+  auto tr_op = [&](auto pitch_tag, uint32_t base, int col0, int ks) -> u32x4 {
+    constexpr int PP = decltype(pitch_tag)::value;
+    const uint32_t tr = 2 * ((4 * h + (s16 >> 2)) * PP + 16 * (g16 & 1) + 4 * (s16 & 3));
+    const uint32_t a = base + tr + 2 * (16 * ks * PP + col0);
+    const u32x2 lo = lds_tr8(a), hi = lds_tr8(a + 2 * 8 * PP);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
-  // acc[mj][ni]: W^T block (j = 64 wj + 32 mj, i = 64 wi + 32 ni)
-  f32x16 acc[2][2];
+  using PX = std::integral_constant<int, XP>;
+  using PG = std::integral_constant<int, kGwP>;
+  // acc[mj][ni]: W^T block (j = 64 wj + 32 mj, i = (FI/2) wi + 32 ni)
+  f32x16 acc[2][NI];
 #pragma unroll
   for (int mj = 0; mj < 2; ++mj)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) acc[mj][ni] = zero16();
+    for (int ni = 0; ni < NI; ++ni) acc[mj][ni] = zero16();
   auto compute = [&](auto two_tag) {
     constexpr bool TWO = decltype(two_tag)::value;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      u32x4 Bx[2], Ah[2], Al[2];
+      u32x4 Bx[NI], Ah[2], Al[2];
+#pragma unroll
+      for (int t = 0; t < NI; ++t) Bx[t] = tr_op(PX{}, sX, FI / 2 * wi + 32 * t, ks);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        Bx[t] = tr_op(sX, 64 * wi + 32 * t, ks);
-        Ah[t] = tr_op(sH, 64 * wj + 32 * t, ks);
-        if (TWO) Al[t] = tr_op(sL, 64 * wj + 32 * t, ks);
+        Ah[t] = tr_op(PG{}, sH, 64 * wj + 32 * t, ks);
+        if (TWO) Al[t] = tr_op(PG{}, sL, 64 * wj + 32 * t, ks);
       }
 #pragma unroll
       for (int mj = 0; mj < 2; ++mj)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
+        for (int ni = 0; ni < NI; ++ni) {
           acc[mj][ni] = mfma(Ah[mj], Bx[ni], acc[mj][ni]);
           if (TWO) acc[mj][ni] = mfma(Al[mj], Bx[ni], acc[mj][ni]);
         }
@@ -395,11 +408,11 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   if (wsel == 0) run(std::true_type{});
   else run(std::false_type{});
 
-  // lane: i = i0 + 64 wi + 32 ni + l32, j = j0 + 64 wj + 32 mj + 8g + 4h + (0..3)
+  // lane: i = i0 + (FI/2) wi + 32 ni + l32, j = j0 + 64 wj + 32 mj + 8g + 4h + (0..3)
   float* dst = part + (size_t)(pbase + chunk) * C * C;
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    float* row = dst + (size_t)(i0 + 64 * wi + 32 * ni + l32) * C + j0 + 64 * wj + 4 * h;
+  for (int ni = 0; ni < NI; ++ni) {
+    float* row = dst + (size_t)(i0 + FI / 2 * wi + 32 * ni + l32) * C + j0 + 64 * wj + 4 * h;
 #pragma unroll
     for (int mj = 0; mj < 2; ++mj)
 #pragma unroll
@@ -446,12 +459,18 @@ void deal(GwShape& sh, int nq_items, int kv_items, bool q_long) {
   sh.short0 = q_long ? nq_items : 0;
 }
 
+// Input-feature tile of computeGradDw: 192 where it divides C (36 -> 24 tiles at C = 768, with
+// fewer operand reads per product), else 128. projBackwarddW's one-weight launch keeps 128: with
+// 24 tiles its row chunks would be a third shorter, and it measured slower.
+int gw_fi(int C) { return C % 192 == 0 ? 192 : 128; }
+
 GwShape grad_dw_shape(int R, int C, int cus) {
   GwShape sh;
   sh.C = C;
-  sh.nt = C / kGwTile;
+  sh.nti = C / gw_fi(C);
+  sh.ntj = C / kGwTile;
   sh.steps = R / kGwK;
-  const int tiles = sh.nt * sh.nt;
+  const int tiles = sh.nti * sh.ntj;
   // as many items per tile as fill one round of two workgroups per CU (k), split so that a dWq
   // item (2 steps / nq products per row step) and a dKw or dVw item (steps / nkv) are as close as
   // k allows: 6 and 4 chunks at C = 768 on 256 CUs (504 items, 85 and 64 product-steps)
@@ -468,9 +487,10 @@ GwShape grad_dw_shape(int R, int C, int cus) {
 GwShape grad_dw_one_shape(int R, int C, int cus) {
   GwShape sh;
   sh.C = C;
-  sh.nt = C / kGwTile;
+  sh.nti = C / kGwTile;
+  sh.ntj = C / kGwTile;
   sh.steps = R / kGwK;
-  const int tiles = sh.nt * sh.nt;
+  const int tiles = sh.nti * sh.ntj;
   sh.nq = 0;
   sh.nkv = std::max(1, std::min(2 * cus / tiles, sh.steps / 2));
   sh.items = tiles * sh.nkv;
@@ -502,7 +522,8 @@ size_t grad_dw_partial_floats(int R, int C) {
 hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV, float* dQw,
                           uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, bool accumulate, hipStream_t s) {
   const GwShape sh = grad_dw_shape(R, C, device_cus());
-  hipLaunchKernelGGL(grad_dw_kernel, dim3((unsigned)sh.items), dim3(256), 0, s, X, dQ, dK, dV, partial, sh);
+  hipLaunchKernelGGL(gw_fi(C) == 192 ? grad_dw_kernel<192> : grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0,
+                     s, X, dQ, dK, dV, partial, sh);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n4 = 3 * (size_t)C * C / 4;
@@ -519,7 +540,7 @@ size_t grad_dw_one_partial_floats(int R, int C) {
 hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
                               bool accumulate, hipStream_t s) {
   const GwShape sh = grad_dw_one_shape(R, C, device_cus());
-  hipLaunchKernelGGL(grad_dw_kernel, dim3((unsigned)sh.items), dim3(256), 0, s, X, nullptr, G, G, partial, sh);
+  hipLaunchKernelGGL(grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0, s, X, nullptr, G, G, partial, sh);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n4 = (size_t)C * C / 4;
