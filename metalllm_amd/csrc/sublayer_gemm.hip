@@ -435,6 +435,8 @@ __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __rest
     const size_t o = 4 * (e - (size_t)(w - w0) * n4);
     const int p0 = w == 0 ? 0 : nq + (w - 1) * nkv, np = w == 0 ? nq : nkv;
     f32x4 acc = *(const f32x4*)(part + (size_t)p0 * cc + o);
+    // unrolled so that several partials' loads are in flight; the adds stay in chunk order
+#pragma unroll 4
     for (int p = 1; p < np; ++p) acc += *(const f32x4*)(part + (size_t)(p0 + p) * cc + o);
     if (w == 0) {
       f32x4* d = (f32x4*)(dQw + o);
