@@ -211,17 +211,19 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
 
 // ---- computeGradDw (attention.metal:343-383): dWq += X^T.dQ (fp32), dKw += X^T.dK, dVw += X^T.dV
 // (bf16), X bf16 [R, C], dQ fp32, dK and dV bf16 [R, C]; the sums run over all R rows into C x C
-// outputs, too few 128 x 128 tiles to fill the chip, so the rows are split into chunks. A work
-// item is one tile of one weight over one chunk of rows, written as an fp32 partial; dWq items
-// run two products per row (hi and lo of dQ, split in registers as in grad_dx_kernel) over half
-// as many rows, so every item has the same matrix-core work. grad_dw_reduce_kernel then adds the
-// partials and the destination's previous value once and rounds once.
+// outputs, too few tiles to fill the chip, so the rows are split into chunks. A work item is one
+// tile (128 output features j x FI input features i) of one weight over one chunk of rows,
+// written as an fp32 partial; dWq items run two products per row (hi and lo of dQ, split in
+// registers as in grad_dx_kernel), and the chunk counts of dWq and of dKw/dVw are chosen so that
+// the two kinds of item carry nearly the same matrix-core work (grad_dw_shape).
+// grad_dw_reduce_kernel then adds the partials and the destination's previous value once and
+// rounds once.
 //
 // Operands: the tile is computed transposed, W^T = G^T . X (m = j, n = i, k = r), so each lane
 // ends with four consecutive j of one i, stored as 16-byte words of the row-major partial. Both
-// operands need 8 rows r of one column per lane: they come from row-major LDS tiles [r][128
-// columns] by ds_read_b64_tr_b16 (pitch 160 elements: the 4 rows x 64 bytes read by 32 lanes of
-// one transposing read fall in distinct banks).
+// operands need 8 rows r of one column per lane: they come from row-major LDS tiles [r][128 or FI
+// columns] by ds_read_b64_tr_b16 (pitch 160 or FI + 32 elements: the 4 rows x 64 bytes read by 32
+// lanes of one transposing read fall in distinct banks).
 constexpr int kGwTile = 128;                     // output features j per tile (and the narrower i width)
 constexpr int kGwK = 64;                         // rows r per step
 constexpr int kGwP = kGwTile + 32;               // LDS row pitch of a 128-column tile (elements)

@@ -62,14 +62,16 @@ def test_forward_gemms(gpu, S):
     assert bad == 0
 
 
-@pytest.mark.parametrize("B,T,H,C", [(2, 256, 12, 768), (1, 384, 3, 384), (1, 320, 5, 200)])
+@pytest.mark.parametrize("B,T,H,C", [(2, 256, 12, 768), (1, 384, 3, 384), (1, 256, 4, 512), (1, 320, 5, 200)])
 def test_backward_gemms(gpu, S, B, T, H, C):
     """R and C multiples of 128 run the hand-written computeGradDx and computeGradDw kernels (fp32
-    dQ split in registers); the last shape runs the library path on the split dQ. For
-    computeGradDw, R=512, C=768 gives 504 work items (6 dWq and 4 dKw/dVw row chunks per tile,
-    the long dWq items dealt to each XCD first) and R=384, C=384 gives 108 (not a multiple of 8:
-    workgroup order) with dWq chunks of one 64-row step; projBackwarddW takes 144 and 27 one-weight
-    items. All are called twice, so the second call accumulates into nonzero destinations."""
+    dQ split in registers), with 192-wide feature tiles where 192 divides C (768, 384) and 128-wide
+    ones otherwise (512); the last shape runs the library path on the split dQ. For computeGradDw,
+    R=512, C=768 gives 24 tiles of 128 x 192 with 8 dWq and 4 dKw/dVw row chunks each (384 items,
+    dealt to the XCDs in contiguous ranges), R=384, C=384 gives 72 (not a multiple of 8 per kind:
+    workgroup order) with dWq chunks of one 64-row step, and R=256, C=512 gives 16 tiles of 128 x
+    128; projBackwarddW (128-wide tiles) takes 144, 27 and 32 one-weight items. All are called
+    twice, so the second call accumulates into nonzero destinations."""
     import torch
     R = B * T
     X, (Wq, Wk, Wv, Wp) = inputs(R, C, 2)
