@@ -141,8 +141,10 @@ int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d, const floa
  * Plain GEMMs with the reference kernels' names and buffer order. Row-major: X, attn_out (O), dZ,
  * q, k, v, dK, dV, dAttn, out are bf16 [B*M, N]; dQ and dX are fp32 [B*M, N]; weights (q_w, k_w,
  * v_w, proj_w and their gradients) are bf16 [N, N] indexed [input feature][output feature], dQw
- * fp32 [N, N]. Products are computed with fp32 accumulation (rocBLAS gemm_ex) and rounded once to
- * the destination type. The "accumulate" kernels read their destination once and add to it, as
+ * fp32 [N, N]. Products are computed with fp32 accumulation and rounded once to the destination
+ * type: computeQKV, projForward and projBackwarddX on rocBLAS gemm_ex; computeGradDx,
+ * computeGradDw and projBackwarddW on hand-written kernels when B*M and N are multiples of 128
+ * (rocBLAS otherwise). The "accumulate" kernels read their destination once and add to it, as
  * the reference's multiply_accumulate matmuls do; the caller zeroes those destinations first
  * (model.h:549-555). Validation: M, B, NH, D >= 1, N == NH*D a multiple of 8, tensors below 2^31
  * elements, non-NULL 16-byte aligned pointers. The first call on a device creates that device's
