@@ -117,7 +117,8 @@ def bench_sublayer(args):
     gen.manual_seed(4321)
     rn = lambda shape, sc=1.0: (torch.randn(shape, generator=gen, device=dev) * sc).to(torch.bfloat16)
     X = rn((B, T, C))
-    Ws = [rn((C, C), 0.02) for _ in range(4)]
+    # q_w, k_w, v_w as slices of one fused [3, C, C] weight (computeQKV then runs one batched product)
+    Ws = list(rn((3, C, C), 0.02).unbind(0)) + [rn((C, C), 0.02)]
     dOut = rn((B, T, C))
     sub = S.Sublayer(X, *Ws, H=H)
     stream = torch.cuda.current_stream()

@@ -163,7 +163,10 @@ int flashAttentionBackwardNoAlloc(const uint16_t* dZ, const float* d, const floa
  * No counterpart in the reference (model.h allocates every buffer once, :236-277). */
 int metalllmSublayerReserve(const AttentionParams* p);
 
-/* attention.metal:19-53, dispatched at model.h:446-457: q = X.q_w, k = X.k_w, v = X.v_w. */
+/* attention.metal:19-53, dispatched at model.h:446-457: q = X.q_w, k = X.k_w, v = X.v_w. When
+ * q_w, k_w, v_w are equally spaced in memory (e.g. slices of one [3][N][N] weight) and q, k, v
+ * are equally spaced without overlapping (e.g. slices of one [3][B*M][N] buffer), the three
+ * products run as one batched library call, which is faster; any other layout runs three. */
 int computeQKV(const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w, const uint16_t* k_w,
                const uint16_t* v_w, const AttentionParams* p, metalllm_stream_t stream);
 

@@ -157,7 +157,11 @@ class Sublayer:
         D = C // H
         dev = X.device
         bf = lambda: torch.empty((B, T, C), dtype=torch.bfloat16, device=dev)
-        self.q, self.k, self.v, self.o, self.out = bf(), bf(), bf(), bf(), bf()
+        # q, k, v as three equal slices of one buffer: with a fused [3, C, C] weight (equally spaced
+        # q_w, k_w, v_w) computeQKV runs one batched product
+        self.qkv = torch.empty((3, B, T, C), dtype=torch.bfloat16, device=dev)
+        self.q, self.k, self.v = self.qkv.unbind(0)
+        self.o, self.out = bf(), bf()
         self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.dO, self.dK, self.dV = bf(), bf(), bf()
         self.Dv = torch.empty((B, H, T), dtype=torch.float32, device=dev)

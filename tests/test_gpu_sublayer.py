@@ -40,14 +40,27 @@ def S():
     return S
 
 
-def test_forward_gemms(gpu, S):
+@pytest.mark.parametrize("fused", [False, True])
+def test_forward_gemms(gpu, S, fused):
+    """fused: q_w, k_w, v_w are slices of one [3, C, C] buffer and q, k, v of one [3, R, C] buffer,
+    so computeQKV runs one strided-batched product; otherwise separate buffers and three."""
     import torch
     B, T, H, C = 2, 256, 12, 768
     R = B * T
     X, (Wq, Wk, Wv, Wp) = inputs(R, C, 1)
     p = S.params_of(torch.empty((B, T, C)), H)
     tX, tq_w, tk_w, tv_w, tWp = (to_gpu(a, gpu) for a in (X, Wq, Wk, Wv, Wp))
-    q, k, v = (torch.empty((R, C), dtype=torch.bfloat16, device=gpu) for _ in range(3))
+    if fused:
+        W3 = torch.stack([tq_w, tk_w, tv_w])
+        tq_w, tk_w, tv_w = W3.unbind(0)
+        q, k, v = torch.empty((3, R, C), dtype=torch.bfloat16, device=gpu).unbind(0)
+    else:
+        # a gap after each output and weight, so that they are not equally spaced
+        q, k, v = (torch.empty((R + 64 * i, C), dtype=torch.bfloat16, device=gpu)[:R] for i in range(3))
+        tk_w = torch.cat([tk_w, tk_w[:8]])[:C]
+    P = lambda t: t.data_ptr()
+    spaced = P(tk_w) - P(tq_w) == P(tv_w) - P(tk_w) and P(k) - P(q) == P(v) - P(k)
+    assert spaced == fused  # the layout selects the path under test
     S.computeQKV(tX, q, k, v, tq_w, tk_w, tv_w, p)
     out = torch.empty((R, C), dtype=torch.bfloat16, device=gpu)
     S.projForward(q, tWp, out, p)
