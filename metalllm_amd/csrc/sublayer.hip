@@ -278,8 +278,12 @@ int reduce_into(const Ctx& c, const float* part, int nparts, size_t n, void* dst
 // 256, 66 against 75 us measured. Otherwise three calls.
 int op_qkv(const Ctx& c, const uint16_t* X, uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_w,
            const uint16_t* k_w, const uint16_t* v_w, int R, int C) {
-  const ptrdiff_t dw = k_w - q_w, dy = k - q;
-  if (dw >= 0 && v_w - k_w == dw && dy >= (ptrdiff_t)R * C && v - k == dy) {
+  // distances in bf16 elements, from the integer addresses (the buffers may be separate allocations)
+  const auto at = [](const uint16_t* ptr) { return (intptr_t)(uintptr_t)ptr; };
+  const intptr_t bw = at(k_w) - at(q_w), by = at(k) - at(q);
+  const intptr_t dw = bw / 2, dy = by / 2;
+  if (bw % 2 == 0 && by % 2 == 0 && dw >= 0 && at(v_w) - at(k_w) == bw && dy >= (intptr_t)R * C &&
+      at(v) - at(k) == by) {
     const float alpha = 1.0f, beta = 0.0f;
     // row-major Y_i = X . W_i; column-major Y_i^T = W_i^T . X^T
     const rocblas_status st = rocblas_gemm_strided_batched_ex(
