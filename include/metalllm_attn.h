@@ -281,7 +281,11 @@ typedef struct metalllmSublayerGraph metalllmSublayerGraph;
  *            flashAttentionBackwardWorkspace, computeGradDx, computeGradDw, and
  *            castFloatToBfloat(dX) when dX_bf16 is set. dX, dQw, dKw, dVw and dProjw, which
  *            model.h zeroes before the pass and accumulates into, have one producer each here:
- *            they are written as 0 + the gradient, bit for bit, without being zeroed or read.
+ *            they are written as 0 + the gradient, without being zeroed or read. When B*M and N
+ *            are multiples of 128, dProjw is computed last, in computeGradDw's launch, so the
+ *            four weight gradients are summed over other row chunks than the entry points use
+ *            (equal up to fp32 summation order); every other output equals the entry points'
+ *            chain bit for bit.
  * With the block fields set: phase 0 starts with layernormForward(hidden -> X) and ends with
  * residualAdd(hidden, out -> residual); phase 1 also zeroes ln_dgamma/ln_dbeta, casts dX into
  * dStream, then runs layernormBackward(dStream) and residualAdd(dStream, dOut -> dStream).

@@ -44,6 +44,10 @@ hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK
 size_t grad_dw_one_partial_floats(int R, int C);
 hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
                               bool accumulate, hipStream_t s);
+size_t grad_dw4_partial_floats(int R, int C);
+hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
+                           const uint16_t* Xp, const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw,
+                           uint16_t* dPw, float* partial, int R, int C, bool accumulate, hipStream_t s);
 }  // namespace mla
 
 namespace {
@@ -212,7 +216,8 @@ size_t split_need(int R, int C) {
 // row_chunks(R) products of C x C (twice that for computeGradDw's dQw) on the library path.
 size_t partial_need(int R, int C) {
   if (mla::grad_dw_fused_ok(R, C))
-    return std::max(mla::grad_dw_one_partial_floats(R, C), mla::grad_dw_partial_floats(R, C));
+    return std::max({mla::grad_dw_one_partial_floats(R, C), mla::grad_dw_partial_floats(R, C),
+                     mla::grad_dw4_partial_floats(R, C)});
   return 2 * (size_t)row_chunks(R) * C * C;
 }
 
@@ -547,7 +552,13 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   // dQ, dK and dV in full; the block's layernorm gradients (model.h:545-546), which its backward
   // adds into with atomics, are zeroed here.
   if (block) TRY(zero_buffers(c, {{b->ln_dgamma, (size_t)C * 4}, {b->ln_dbeta, (size_t)C * 4}}));
-  TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial, false));
+  // With the hand-written weight-gradient kernel, dProjw (which nothing in this phase reads) is
+  // computed at the end, as a fourth weight of computeGradDw's launch and reduction: one launch of
+  // balanced items instead of projBackwarddW's own short-item launch. Its sum then runs over
+  // other row chunks than the entry point's, so it can differ from projBackwarddW's result by the
+  // fp32 summation order (one bf16 rounding step at most).
+  const bool fuse_pdw = mla::grad_dw_fused_ok(R, C);
+  if (!fuse_pdw) TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial, false));
   TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
   if (!c.query) {
     TRY(computeD(b->dAttn, b->attn_out, b->Dsum, p, s));
@@ -562,7 +573,13 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
     split = nullptr;
   }
   TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
-  TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial, false));
+  if (fuse_pdw) {
+    if (!c.query && mla::launch_grad_dw4(b->X, b->dQ, b->dK, b->dV, b->attn_out, b->dOut, b->dQw, b->dKw, b->dVw,
+                                         b->dProjw, partial, R, C, false, c.stream) != hipSuccess)
+      return METALLLM_ATTN_E_LAUNCH;
+  } else {
+    TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial, false));
+  }
   if (c.query) return METALLLM_ATTN_OK;
   if (block) {  // model.h:692-695
     TRY(castFloatToBfloat(b->dX, b->dStream, (uint32_t)e, s));

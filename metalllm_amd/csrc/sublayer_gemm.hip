@@ -236,14 +236,15 @@ __device__ __forceinline__ u32x2 lds_tr8(uint32_t a) {
 struct GwShape {
   int C, nti, ntj;  // features; tiles along i (FI wide) and along j (128 wide)
   int steps;        // R / kGwK
-  int nq, nkv;      // row chunks of dWq, and of each of dKw and dVw
-  int items;        // nt^2 (nq + 2 nkv)
+  int nq, nkv;      // row chunks of dWq, and of each bf16 weight (dKw, dVw, and dPw when fused)
+  int items;        // tiles (nq + nb nkv), nb bf16 weights
   // XCD deal (0 in lx: workgroup order): XCD x takes items long0 + x lx + k for k < lx, then
   // short0 + x sx + (k - lx)
   int lx, sx, long0, short0;
 };
 
-// Work items in order (weight, chunk, i block, j block): dWq's, then dKw's, then dVw's.
+// Work items in order (weight, chunk, i block, j block): dWq's, then dKw's, then dVw's, then (the
+// phase encoder's fused form) dPw's, the projection weight's gradient Xp^T . Gp.
 // Workgroups are dealt to the 8 XCDs in turn (blockIdx % 8, workgroup k of an XCD is blockIdx / 8).
 // When 8 divides the item count of each kind, each XCD takes a contiguous range of the longer
 // kind's items first (the kind with more products per item: dWq's or dKw's and dVw's), then a
@@ -253,6 +254,7 @@ struct GwShape {
 template <int FI>
 __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
                                                         const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
+                                                        const uint16_t* __restrict__ Xp, const uint16_t* __restrict__ Gp,
                                                         float* __restrict__ part, GwShape sh) {
   static_assert(FI == 128 || FI == 192, "input-feature tile");
   constexpr int NI = FI / 64;                 // 32-wide i tiles per wave
@@ -281,7 +283,8 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   const int chunk = item / tiles, tile = item - chunk * tiles;
   const int i0 = (tile / sh.ntj) * FI, j0 = (tile % sh.ntj) * kGwTile;
   const int s0 = (int)((long)chunk * sh.steps / nch), s1 = (int)((long)(chunk + 1) * sh.steps / nch);
-  const uint16_t* G = wsel == 1 ? dK : dV;
+  const uint16_t* G = wsel == 1 ? dK : (wsel == 2 ? dV : Gp);
+  const uint16_t* Xs = wsel == 3 ? Xp : X;
   const int wi = wave & 1, wj = wave >> 1;
   const uint32_t sX = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
   const uint32_t sH = sX + XBYTES, sL = sH + kGwTileBytes;
@@ -295,7 +298,7 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
       const int c = tid + 256 * q;
-      xreg[q] = *(const u32x4*)(X + (size_t)(r + c / XCH) * C + i0 + 8 * (c % XCH));
+      xreg[q] = *(const u32x4*)(Xs + (size_t)(r + c / XCH) * C + i0 + 8 * (c % XCH));
     }
   };
   auto load_g = [&](int r) {
@@ -424,13 +427,14 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   }
 }
 
-// dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw = bf16(previous + the sum of
-// their nkv partials). Partials [nq + 2 nkv][C][C]; four consecutive elements per thread. Only the
-// weights w0 .. w0 + nw - 1 (0 dQw, 1 dKw, 2 dVw) are reduced. Without acc the destinations are
-// written as if they held zeros (bit for bit 0 + sum), and not read.
+// dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw, dPw = bf16(previous + the
+// sum of their nkv partials). Partials [nq + nb nkv][C][C]; four consecutive elements per thread.
+// Only the weights w0 .. w0 + nw - 1 (0 dQw, 1 dKw, 2 dVw, 3 dPw) are reduced. Without acc the
+// destinations are written as if they held zeros (bit for bit 0 + sum), and not read.
 __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __restrict__ part, float* __restrict__ dQw,
                                                                uint16_t* __restrict__ dKw, uint16_t* __restrict__ dVw,
-                                                               int C, int nq, int nkv, int w0, int nw, bool acc_dst) {
+                                                               uint16_t* __restrict__ dPw, int C, int nq, int nkv, int w0,
+                                                               int nw, bool acc_dst) {
   const size_t cc = (size_t)C * C, n4 = cc / 4;
   for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < nw * n4; e += (size_t)gridDim.x * blockDim.x) {
     const int w = w0 + (int)(e / n4);
@@ -444,7 +448,7 @@ __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __rest
       f32x4* d = (f32x4*)(dQw + o);
       *d = (acc_dst ? *d : f32x4{0.0f, 0.0f, 0.0f, 0.0f}) + acc;
     } else {
-      u32x2* d = (u32x2*)((w == 1 ? dKw : dVw) + o);
+      u32x2* d = (u32x2*)((w == 1 ? dKw : (w == 2 ? dVw : dPw)) + o);
       const u32x2 old = acc_dst ? *d : u32x2{0u, 0u};
       *d = u32x2{pack_bf16(bf_lo(old[0]) + acc[0], bf_hi(old[0]) + acc[1]),
                  pack_bf16(bf_lo(old[1]) + acc[2], bf_hi(old[1]) + acc[3])};
@@ -452,8 +456,8 @@ __global__ void __launch_bounds__(256) grad_dw_reduce_kernel(const float* __rest
   }
 }
 
-// The XCD deal of GwShape for nq_items dWq items (first in item order) and kv_items dKw and dVw
-// items; q_long: dWq's items carry more products than the others'.
+// The XCD deal of GwShape for nq_items dWq items (first in item order) and kv_items items of the
+// bf16 weights; q_long: dWq's items carry more products than the others'.
 void deal(GwShape& sh, int nq_items, int kv_items, bool q_long) {
   sh.lx = sh.sx = sh.long0 = sh.short0 = 0;
   if (nq_items % 8 || kv_items % 8) return;
@@ -468,7 +472,8 @@ void deal(GwShape& sh, int nq_items, int kv_items, bool q_long) {
 // 24 tiles its row chunks would be a third shorter, and it measured slower.
 int gw_fi(int C) { return C % 192 == 0 ? 192 : 128; }
 
-GwShape grad_dw_shape(int R, int C, int cus) {
+// nb bf16 weights beside dWq: 2 (computeGradDw) or 3 (with dPw, the phase encoder's fused form)
+GwShape grad_dw_shape(int R, int C, int cus, int nb = 2) {
   GwShape sh;
   sh.C = C;
   sh.nti = C / gw_fi(C);
@@ -476,13 +481,14 @@ GwShape grad_dw_shape(int R, int C, int cus) {
   sh.steps = R / kGwK;
   const int tiles = sh.nti * sh.ntj;
   // as many items per tile as fill one round of two workgroups per CU (k), split so that a dWq
-  // item (2 steps / nq products per row step) and a dKw or dVw item (steps / nkv) are as close as
-  // k allows: 6 and 4 chunks at C = 768 on 256 CUs (504 items, 85 and 64 product-steps)
-  const int k = std::max(4, 2 * cus / tiles);
-  sh.nkv = std::max(1, std::min((k + 2) / 4, sh.steps / 2));
-  sh.nq = std::max(1, std::min(k - 2 * sh.nkv, sh.steps));
-  sh.items = tiles * (sh.nq + 2 * sh.nkv);
-  deal(sh, tiles * sh.nq, 2 * tiles * sh.nkv, 2 * sh.nkv > sh.nq);
+  // item (2 steps / nq products per row step) and a bf16-weight item (steps / nkv) are as close as
+  // k allows (nq near 2 nkv): at C = 768 on 256 CUs, k = 21: nq 11, nkv 5 (504 items, 47 and 51
+  // product-steps); with dPw nq 9, nkv 4 (504 items, 57 and 64)
+  const int k = std::max(2 + nb, 2 * cus / tiles);
+  sh.nkv = std::max(1, std::min((k + 2) / (2 + nb), sh.steps / 2));
+  sh.nq = std::max(1, std::min(k - nb * sh.nkv, sh.steps));
+  sh.items = tiles * (sh.nq + nb * sh.nkv);
+  deal(sh, tiles * sh.nq, nb * tiles * sh.nkv, 2 * sh.nkv > sh.nq);
   return sh;
 }
 
@@ -527,12 +533,33 @@ hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK
                           uint16_t* dKw, uint16_t* dVw, float* partial, int R, int C, bool accumulate, hipStream_t s) {
   const GwShape sh = grad_dw_shape(R, C, device_cus());
   hipLaunchKernelGGL(gw_fi(C) == 192 ? grad_dw_kernel<192> : grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0,
-                     s, X, dQ, dK, dV, partial, sh);
+                     s, X, dQ, dK, dV, nullptr, nullptr, partial, sh);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n4 = 3 * (size_t)C * C / 4;
   hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
-                     partial, dQw, dKw, dVw, C, sh.nq, sh.nkv, 0, 3, accumulate);
+                     partial, dQw, dKw, dVw, nullptr, C, sh.nq, sh.nkv, 0, 3, accumulate);
+  return hipGetLastError();
+}
+
+// computeGradDw and projBackwarddW in one launch and one reduction (the phase encoder): dPw =
+// Xp^T . Gp (attn_out^T . dZ) as a fourth weight.
+size_t grad_dw4_partial_floats(int R, int C) {
+  const GwShape sh = grad_dw_shape(R, C, device_cus(), 3);
+  return (size_t)(sh.nq + 3 * sh.nkv) * C * C;
+}
+
+hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
+                           const uint16_t* Xp, const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw,
+                           uint16_t* dPw, float* partial, int R, int C, bool accumulate, hipStream_t s) {
+  const GwShape sh = grad_dw_shape(R, C, device_cus(), 3);
+  hipLaunchKernelGGL(gw_fi(C) == 192 ? grad_dw_kernel<192> : grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0,
+                     s, X, dQ, dK, dV, Xp, Gp, partial, sh);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n4 = 4 * (size_t)C * C / 4;
+  hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
+                     partial, dQw, dKw, dVw, dPw, C, sh.nq, sh.nkv, 0, 4, accumulate);
   return hipGetLastError();
 }
 
@@ -544,12 +571,13 @@ size_t grad_dw_one_partial_floats(int R, int C) {
 hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
                               bool accumulate, hipStream_t s) {
   const GwShape sh = grad_dw_one_shape(R, C, device_cus());
-  hipLaunchKernelGGL(grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0, s, X, nullptr, G, G, partial, sh);
+  hipLaunchKernelGGL(grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0, s, X, nullptr, G, G, nullptr, nullptr,
+                     partial, sh);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n4 = (size_t)C * C / 4;
   hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
-                     partial, nullptr, dW, nullptr, C, 0, sh.nkv, 1, 1, accumulate);
+                     partial, nullptr, dW, nullptr, nullptr, C, 0, sh.nkv, 1, 1, accumulate);
   return hipGetLastError();
 }
 

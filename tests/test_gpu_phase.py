@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 from tests.attn_case import to_gpu, to_np
-from tests.sublayer_check import check_sublayer
+from tests.sublayer_check import WEIGHT_GRADS, check_sublayer, same_up_to_order
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +66,8 @@ def _snapshot(sub):
 
 def test_encoder_matches_per_call_chain(gpu, S):
     """metalllmSublayerEncode(0), (1) == the chain of public entry points (model.h order), bit for
-    bit, and its dX_bf16 is castFloatToBfloat(dX)."""
+    bit except the weight gradients (summation order, same_up_to_order), and its dX_bf16 is
+    castFloatToBfloat(dX)."""
     import torch
     B, T, H, C = 2, 512, 12, 768
     a, dOut = _sublayer(S, gpu, B, T, H, C, 21)
@@ -85,6 +86,9 @@ def test_encoder_matches_per_call_chain(gpu, S):
     for n in OUTPUTS:
         same = np.array_equal(ra[n], rb[n])
         print(f"{n}: {'identical' if same else 'DIFFERENT'}")
+        if n in WEIGHT_GRADS and not same:
+            same = same_up_to_order(n, rb[n], ra[n])
+            print(f"  {n} within the summation-order bar: {same}")
         assert same, n
     assert np.array_equal(rb["dXb"], O.castFloatToBfloat(rb["dX"]))
     # and the encoder's own results against the oracle, stage by stage
@@ -125,7 +129,8 @@ def test_graph_replays_match_encoder(gpu, S):
 def test_block_half_encoder_and_graphs(gpu, S):
     """The block's attention half (ln1, sublayer, residual add; backward with the dX cast, ln1
     backward and the skip add) through the encoder and as graphs equals the same sequence issued
-    through the public entry points (model.h:445-483, 617-695), bit for bit."""
+    through the public entry points (model.h:445-483, 617-695), bit for bit except the weight
+    gradients (summation order, same_up_to_order)."""
     import torch
     import metalllm_amd.glue as G
     B, T, H, C = 2, 256, 6, 384
@@ -159,7 +164,10 @@ def test_block_half_encoder_and_graphs(gpu, S):
              ("out", blk.out, ref.out), ("residual", blk.residual, residual), ("dX", blk.dX, ref.dX),
              ("dWq", blk.dWq, ref.dWq), ("dWp", blk.dWp, ref.dWp), ("dStream", blk.dStream, dStream)]
     for name, a, b in pairs:
-        assert torch.equal(a, b), name
+        if name in WEIGHT_GRADS:
+            assert same_up_to_order(name, a, b), name
+        else:
+            assert torch.equal(a, b), name
     # dgamma/dbeta: fp32 column sums added with atomics (order varies between runs)
     for name, a, b in (("dgamma", blk.ln_dgamma, dg), ("dbeta", blk.ln_dbeta, db)):
         assert (a - b).abs().max().item() <= 1e-5 * b.abs().max().item(), name
