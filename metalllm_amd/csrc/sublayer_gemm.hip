@@ -217,7 +217,9 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
 // registers as in grad_dx_kernel), and the chunk counts of dWq and of dKw/dVw are chosen so that
 // the two kinds of item carry nearly the same matrix-core work (grad_dw_shape).
 // grad_dw_reduce_kernel then adds the partials and the destination's previous value once and
-// rounds once.
+// rounds once. projBackwarddW (attention.metal:407-430, dProjw += attn_out^T.dZ) runs the same
+// kernel with one bf16 weight (grad_dw_one_shape), and the phase encoder adds it to
+// computeGradDw's launch as a fourth weight (Xp = attn_out, Gp = dZ; launch_grad_dw4).
 //
 // Operands: the tile is computed transposed, W^T = G^T . X (m = j, n = i, k = r), so each lane
 // ends with four consecutive j of one i, stored as 16-byte words of the row-major partial. Both
@@ -247,7 +249,7 @@ struct GwShape {
 // phase encoder's fused form) dPw's, the projection weight's gradient Xp^T . Gp.
 // Workgroups are dealt to the 8 XCDs in turn (blockIdx % 8, workgroup k of an XCD is blockIdx / 8).
 // When 8 divides the item count of each kind, each XCD takes a contiguous range of the longer
-// kind's items first (the kind with more products per item: dWq's or dKw's and dVw's), then a
+// kind's items first (the kind with more products per item: dWq's or the bf16 weights'), then a
 // contiguous range of the other kind's: the items that share a chunk's rows run on one XCD and
 // share its L2, and an XCD's first workgroups, which start one on each CU, carry the long items,
 // so that a CU's second workgroup is a short one.
