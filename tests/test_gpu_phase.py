@@ -95,6 +95,21 @@ def test_encoder_matches_per_call_chain(gpu, S):
     check_sublayer(b, to_np(dOut), batches=[0, 1], label="encoder")
 
 
+@pytest.mark.parametrize("B,T,H,C", [(1, 128, 2, 256), (1, 256, 6, 384), (1, 384, 5, 640), (2, 320, 8, 1024)])
+def test_encoder_shapes_against_oracle(gpu, S, B, T, H, C):
+    """The phase encoder at more shapes, every stage against the oracle: the weight-gradient
+    launch of all four weights with its chunk split and item order at each (C = 256, 640, 1024:
+    128-wide tiles; 384: 192-wide; items dealt to the XCDs long-first at C = 1024, in workgroup
+    order at the others), D = 64 and 128, sequence lengths that are and are not multiples of 128."""
+    import torch
+    sub, dOut = _sublayer(S, gpu, B, T, H, C, 51)
+    sub.dOut.copy_(dOut)
+    sub.encode(0)
+    sub.encode(1)
+    torch.cuda.synchronize()
+    check_sublayer(sub, to_np(dOut), batches=[B - 1], label=f"encoder {(B, T, H, C)}")
+
+
 def test_graph_replays_match_encoder(gpu, S):
     """Both phases recorded as graphs replay bit-identically to the eager encoder on new inputs,
     three times, with eager work and synchronisations between the replays; one config-4 shape
