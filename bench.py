@@ -99,18 +99,21 @@ def cpu_baseline(B, H, T, D, qk_scale, threads, target_s=10.0):
     }
 
 
-def bench_sublayer(args):
+def bench_sublayer(args, shape=(8, 2048, 768, 12), label="config4"):
     """one pre-LN block's attention sublayer, fwd + bwd, X bf16 [8, 2048, 768]
     ~N(0,1), Wq/Wk/Wv/Wproj bf16 [768, 768] ~N(0, 0.02), dOut ~N(0,1), H=12 (D=64). One step =
     forward computeQKV -> flashAttentionForward -> projForward and backward projBackwarddW/dX ->
     computeD -> flashAttentionBackward -> computeGradDx/Dw (model.h:446-482, 621-690), with the
     accumulated gradients starting from zero (model.h:549-555). The per-call chain (timed per phase
     by events) zeroes them and adds into them; the headline, the phase encoder, writes them as
-    0 + the gradient. Returns the result object (ms per step and the attention share)."""
+    0 + the gradient. Returns the result object (ms per step and the attention share).
+    `shape` = (B, T, C, H) runs the same chain at another shape; (128, 256, 384, 6) is config 1's
+    attention shape (metalLLM's own N_EMBED = 384, 6 heads), where the step is short enough for the
+    host's launch cost to show between the per-call chain, the encoder and the graphs."""
     import torch
     import metalllm_amd as M
     from metalllm_amd import sublayer as S
-    B, T, C, H = 8, 2048, 768, 12
+    B, T, C, H = shape
     D = C // H
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -187,7 +190,7 @@ def bench_sublayer(args):
     ms = ms_encode
     sub.close()
     return {
-        "metric": "attention sublayer fwd+bwd ms per step (config 4), with the attention share",
+        "metric": f"attention sublayer fwd+bwd ms per step ({label}), with the attention share",
         "value": round(ms, 4),
         "unit": "ms",
         "n_gpus": 1,
@@ -199,7 +202,7 @@ def bench_sublayer(args):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "config4: pre-LN attention sublayer fwd+bwd (QKV, causal flash attention, "
+        "config": {"workload": f"{label}: pre-LN attention sublayer fwd+bwd (QKV, causal flash attention, "
                                "projection; their gradients)", "B": B, "T": T, "C": C, "H": H, "D": D},
         "step_mode": "phase encoder (metalllmSublayerEncode, one call per phase)",
         "modes_ms_per_step": {"graph": round(ms_graph, 4), "encoder": round(ms_encode, 4),
@@ -361,6 +364,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4],
                     help="1-3: attention core (fwd + computeD + bwd); 4: the whole attention sublayer")
+    ap.add_argument("--sublayer-shape", default=None, metavar="B,T,C,H",
+                    help="with --config 4: run the sublayer chain at this shape instead of config 4's "
+                         "(e.g. 128,256,384,6, config 1's attention shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the other BASELINE configs that the default run measures beside the headline")
@@ -379,7 +385,14 @@ def main():
     import metalllm_amd as M  # noqa: F401
 
     if args.config == 4:
-        print(json.dumps(bench_sublayer(args)), flush=True)
+        if args.sublayer_shape:
+            shape = tuple(int(x) for x in args.sublayer_shape.split(","))
+            if len(shape) != 4:
+                ap.error("--sublayer-shape takes B,T,C,H")
+            r = bench_sublayer(args, shape=shape, label="config4 chain at B,T,C,H = " + args.sublayer_shape)
+        else:
+            r = bench_sublayer(args)
+        print(json.dumps(r), flush=True)
         return
     r = run_core(args.config, args.steps, args.warmup, args.calibrate_copy)
     B, H, T, D, qk_scale, desc = r["shape"]
@@ -529,8 +542,12 @@ def main():
             if cid != args.config:
                 extra[f"config{cid}"] = core_summary(cid, run_core(cid, args.steps, args.warmup))
         c4 = bench_sublayer(args)
-        extra["config4"] = {k: c4[k] for k in ("config", "ms_per_step", "step_mode", "modes_ms_per_step",
-                                               "attention_share", "phases_ms_median", "tflops")}
+        keys = ("config", "ms_per_step", "step_mode", "modes_ms_per_step", "attention_share",
+                "phases_ms_median", "tflops")
+        extra["config4"] = {k: c4[k] for k in keys}
+        # the same sublayer at config 1's shape: the short step where launch cost can show
+        c4s = bench_sublayer(args, shape=(128, 256, 384, 6), label="config4 chain at config 1's shape")
+        extra["config4_at_config1_shape"] = {k: c4s[k] for k in keys}
         result["extra_configs"] = extra
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(B, H, T, D, qk_scale, args.cpu_threads)
