@@ -179,3 +179,28 @@ def test_config4_full_size(gpu, S):
         assert torch.equal(getattr(sub, n), getattr(enc, n)), n
     for n in WEIGHT_GRADS:  # the encoder's fused weight-gradient launch sums in another order
         assert same_up_to_order(n, getattr(enc, n), getattr(sub, n)), n
+
+
+def test_config4_chain_at_config1_shape(gpu, S):
+    """The config 4 chain at bench.py's second sublayer shape, metalLLM's own width with config 1's
+    batch and length: B=128, T=256, C=384, H=6 (D=64), R = 32768 rows. The weight gradients run
+    the hand-written kernel's 510 items (43 dWq and 21 dKw/dVw row chunks per 128 x 192 tile; 34
+    and 17 in the encoder's four-weight launch), the attention backward the fused short-sequence
+    kernel (768 pairs). Row-local stages are checked on batches 0 and 127, the weight gradients over
+    all rows; the phase encoder must give the per-call chain's results bit for bit, except the
+    weight gradients (same_up_to_order)."""
+    import torch
+    B, T, H, C = 128, 256, 6, 384
+    print(f"case config4 chain B={B} T={T} H={H} C={C}", flush=True)
+    S.reserve(S.params_of(torch.empty((B, T, C)), H))
+    sub, dOut = _run_chain(S, gpu, B, T, H, C, 9)
+    check_sublayer(sub, dOut, batches=[0, 127], label="config4 chain at c1 shape")
+    enc = S.Sublayer(sub.X, sub.Wq, sub.Wk, sub.Wv, sub.Wp, H=H)
+    enc.dOut.copy_(to_gpu(dOut.reshape(B, T, C), gpu))
+    enc.encode(0)
+    enc.encode(1)
+    torch.cuda.synchronize()
+    for n in ("q", "k", "v", "o", "lse", "out", "dO", "Dv", "dQ", "dK", "dV", "dX"):
+        assert torch.equal(getattr(sub, n), getattr(enc, n)), n
+    for n in WEIGHT_GRADS:
+        assert same_up_to_order(n, getattr(enc, n), getattr(sub, n)), n
