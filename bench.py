@@ -387,8 +387,8 @@ def main():
     if args.config == 4:
         if args.sublayer_shape:
             shape = tuple(int(x) for x in args.sublayer_shape.split(","))
-            if len(shape) != 4:
-                ap.error("--sublayer-shape takes B,T,C,H")
+            if len(shape) != 4 or min(shape) < 1 or shape[2] % shape[3]:
+                ap.error("--sublayer-shape takes B,T,C,H: positive, with H dividing C")
             r = bench_sublayer(args, shape=shape, label="config4 chain at B,T,C,H = " + args.sublayer_shape)
         else:
             r = bench_sublayer(args)
