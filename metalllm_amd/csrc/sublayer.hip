@@ -48,6 +48,10 @@ size_t grad_dw4_partial_floats(int R, int C);
 hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
                            const uint16_t* Xp, const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw,
                            uint16_t* dPw, float* partial, int R, int C, bool accumulate, hipStream_t s);
+hipError_t launch_grad_dxdw4(float* dX, const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
+                             const uint16_t* Wq, const uint16_t* Wk, const uint16_t* Wv, const uint16_t* Xp,
+                             const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw, uint16_t* dPw, float* partial,
+                             int R, int C, hipStream_t s);
 }  // namespace mla
 
 namespace {
@@ -572,12 +576,20 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   } else {
     split = nullptr;
   }
-  TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
-  if (fuse_pdw) {
+  if (fuse_pdw && mla::grad_dx_fused_ok(R, C)) {
+    // computeGradDx and the four weight gradients in one launch (dX tiles first, then the
+    // weight-gradient items, which start as the dX tiles finish), then the reduction
+    if (!c.query && mla::launch_grad_dxdw4(b->dX, b->X, b->dQ, b->dK, b->dV, b->q_w, b->k_w, b->v_w, b->attn_out,
+                                           b->dOut, b->dQw, b->dKw, b->dVw, b->dProjw, partial, R, C,
+                                           c.stream) != hipSuccess)
+      return METALLLM_ATTN_E_LAUNCH;
+  } else if (fuse_pdw) {
+    TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
     if (!c.query && mla::launch_grad_dw4(b->X, b->dQ, b->dK, b->dV, b->attn_out, b->dOut, b->dQw, b->dKw, b->dVw,
                                          b->dProjw, partial, R, C, false, c.stream) != hipSuccess)
       return METALLLM_ATTN_E_LAUNCH;
   } else {
+    TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
     TRY(op_grad_dw(c, b->X, b->dQ, split, lo, b->dK, b->dV, b->dQw, b->dKw, b->dVw, R, C, partial, false));
   }
   if (c.query) return METALLLM_ATTN_OK;

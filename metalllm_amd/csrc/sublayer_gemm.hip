@@ -45,16 +45,20 @@ __device__ __forceinline__ void lds_st8(uint32_t a, u32x2 v) { *(__attribute__((
 
 // ACC: dX += the products (the reference's contract); otherwise dX = 0 + the products, written
 // without reading dX (the phase encoder, which would zero dX just before).
+template <int FI>
+constexpr int grad_dx_smem() { return FI * kGxP * 2 + 2 * kGxTileBytes; }  // W, G hi, G lo
+
+// The kernel's body on the LDS at smem (grad_dx_smem<FI>() bytes), as workgroup bid of the grid.
 template <bool ACC, int FI>
-__global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX, const float* __restrict__ dQ,
-                                                        const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
-                                                        const uint16_t* __restrict__ Wq, const uint16_t* __restrict__ Wk,
-                                                        const uint16_t* __restrict__ Wv, int C, int items) {
+__device__ __forceinline__ void grad_dx_body(unsigned char* smem, int bid, float* __restrict__ dX,
+                                             const float* __restrict__ dQ, const uint16_t* __restrict__ dK,
+                                             const uint16_t* __restrict__ dV, const uint16_t* __restrict__ Wq,
+                                             const uint16_t* __restrict__ Wk, const uint16_t* __restrict__ Wv, int C,
+                                             int items) {
   static_assert(FI == 128 || FI == 192, "feature tile");
   constexpr int MI = FI / 64;                          // 32-wide i tiles per wave
   constexpr int WQ = FI / 32;                          // W tile chunks per thread
   constexpr int WBYTES = FI * kGxP * 2;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[WBYTES + 2 * kGxTileBytes];  // W, G hi, G lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
@@ -62,7 +66,7 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
   // (blockIdx % 8); when 8 divides the tile count each XCD takes a contiguous range of tiles, so
   // the C/FI tiles that read the same gradient rows run together on one XCD and share its L2.
   const int nfb = C / FI;
-  const int item = items % 8 == 0 ? (int)(blockIdx.x % 8) * (items / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int item = items % 8 == 0 ? (bid % 8) * (items / 8) + bid / 8 : bid;
   const int r0 = (item / nfb) * kGxTile, i0 = (item % nfb) * FI;
   const int wi = wave & 1, wr = wave >> 1;
   const uint32_t sW = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)smem;
@@ -209,6 +213,15 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
   }
 }
 
+template <bool ACC, int FI>
+__global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX, const float* __restrict__ dQ,
+                                                        const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
+                                                        const uint16_t* __restrict__ Wq, const uint16_t* __restrict__ Wk,
+                                                        const uint16_t* __restrict__ Wv, int C, int items) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[grad_dx_smem<FI>()];
+  grad_dx_body<ACC, FI>(smem, (int)blockIdx.x, dX, dQ, dK, dV, Wq, Wk, Wv, C, items);
+}
+
 // ---- computeGradDw (attention.metal:343-383): dWq += X^T.dQ (fp32), dKw += X^T.dK, dVw += X^T.dV
 // (bf16), X bf16 [R, C], dQ fp32, dK and dV bf16 [R, C]; the sums run over all R rows into C x C
 // outputs, too few tiles to fill the chip, so the rows are split into chunks. A work item is one
@@ -254,24 +267,26 @@ struct GwShape {
 // share its L2, and an XCD's first workgroups, which start one on each CU, carry the long items,
 // so that a CU's second workgroup is a short one.
 template <int FI>
-__global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
-                                                        const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
-                                                        const uint16_t* __restrict__ Xp, const uint16_t* __restrict__ Gp,
-                                                        float* __restrict__ part, GwShape sh) {
+constexpr int grad_dw_smem() { return kGwK * (FI + 32) * 2 + 2 * kGwTileBytes; }  // X, G (dQ hi), dQ lo
+
+template <int FI>
+__device__ __forceinline__ void grad_dw_body(unsigned char* smem, int bid, const uint16_t* __restrict__ X,
+                                             const float* __restrict__ dQ, const uint16_t* __restrict__ dK,
+                                             const uint16_t* __restrict__ dV, const uint16_t* __restrict__ Xp,
+                                             const uint16_t* __restrict__ Gp, float* __restrict__ part, const GwShape& sh) {
   static_assert(FI == 128 || FI == 192, "input-feature tile");
   constexpr int NI = FI / 64;                 // 32-wide i tiles per wave
   constexpr int XQ = FI / 32;                 // X tile chunks per thread
   constexpr int XCH = FI / 8;                 // 16-byte chunks per X row
   constexpr int XP = FI + 32;                 // X tile pitch (elements)
   constexpr int XBYTES = kGwK * XP * 2;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[XBYTES + 2 * kGwTileBytes];  // X, G (dQ hi), dQ lo
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31, g16 = lane >> 4, s16 = lane & 15;
   const int C = sh.C, tiles = sh.nti * sh.ntj;
-  int item = (int)blockIdx.x;
+  int item = bid;
   if (sh.lx) {
-    const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
+    const int x = bid % 8, k = bid / 8;
     item = k < sh.lx ? sh.long0 + x * sh.lx + k : sh.short0 + x * sh.sx + (k - sh.lx);
   }
   int wsel = 0, nch = sh.nq, pbase = 0;
@@ -429,6 +444,34 @@ __global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restr
   }
 }
 
+template <int FI>
+__global__ void __launch_bounds__(256, 2) grad_dw_kernel(const uint16_t* __restrict__ X, const float* __restrict__ dQ,
+                                                        const uint16_t* __restrict__ dK, const uint16_t* __restrict__ dV,
+                                                        const uint16_t* __restrict__ Xp, const uint16_t* __restrict__ Gp,
+                                                        float* __restrict__ part, GwShape sh) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[grad_dw_smem<FI>()];
+  grad_dw_body<FI>(smem, (int)blockIdx.x, X, dQ, dK, dV, Xp, Gp, part, sh);
+}
+
+// computeGradDx (written, not accumulated) and the four-weight computeGradDw in one launch (the
+// phase encoder): workgroups [0, nx) take computeGradDx's items and the rest computeGradDw's, so
+// that the weight-gradient items start on the CUs whose dX tiles are done while the other dX
+// tiles' stores drain. Where 8 divides nx both parts keep their XCD deal (else only their L2
+// sharing changes, not the results).
+template <int FI>
+__global__ void __launch_bounds__(256, 2) grad_dxdw_kernel(float* __restrict__ dX, const uint16_t* __restrict__ X,
+                                                          const float* __restrict__ dQ, const uint16_t* __restrict__ dK,
+                                                          const uint16_t* __restrict__ dV, const uint16_t* __restrict__ Wq,
+                                                          const uint16_t* __restrict__ Wk, const uint16_t* __restrict__ Wv,
+                                                          const uint16_t* __restrict__ Xp, const uint16_t* __restrict__ Gp,
+                                                          float* __restrict__ part, int nx, GwShape sh) {
+  constexpr int SM = grad_dx_smem<FI>() > grad_dw_smem<FI>() ? grad_dx_smem<FI>() : grad_dw_smem<FI>();
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SM];
+  const int bid = (int)blockIdx.x;
+  if (bid < nx) grad_dx_body<false, FI>(smem, bid, dX, dQ, dK, dV, Wq, Wk, Wv, sh.C, nx);
+  else grad_dw_body<FI>(smem, bid - nx, X, dQ, dK, dV, Xp, Gp, part, sh);
+}
+
 // dQw += the sum of its nq partials (fp32, in chunk order); dKw, dVw, dPw = bf16(previous + the
 // sum of their nkv partials). Partials [nq + nb nkv][C][C]; four consecutive elements per thread.
 // Only the weights w0 .. w0 + nw - 1 (0 dQw, 1 dKw, 2 dVw, 3 dPw) are reduced. Without acc the
@@ -562,6 +605,26 @@ hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* d
   const size_t n4 = 4 * (size_t)C * C / 4;
   hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
                      partial, dQw, dKw, dVw, dPw, C, sh.nq, sh.nkv, 0, 4, accumulate);
+  return hipGetLastError();
+}
+
+// The phase encoder's computeGradDx (dX written) and four-weight computeGradDw in one launch,
+// then the reduction; the shapes of launch_grad_dx and launch_grad_dw4 (feature tiles of the same
+// width: 192 where it divides C, else 128).
+hipError_t launch_grad_dxdw4(float* dX, const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
+                             const uint16_t* Wq, const uint16_t* Wk, const uint16_t* Wv, const uint16_t* Xp,
+                             const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw, uint16_t* dPw, float* partial,
+                             int R, int C, hipStream_t s) {
+  const GwShape sh = grad_dw_shape(R, C, device_cus(), 3);
+  const bool wide = gw_fi(C) == 192;
+  const int nx = (R / kGxTile) * (C / (wide ? 192 : 128));
+  hipLaunchKernelGGL(wide ? grad_dxdw_kernel<192> : grad_dxdw_kernel<128>, dim3((unsigned)(nx + sh.items)), dim3(256), 0,
+                     s, dX, X, dQ, dK, dV, Wq, Wk, Wv, Xp, Gp, partial, nx, sh);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n4 = 4 * (size_t)C * C / 4;
+  hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
+                     partial, dQw, dKw, dVw, dPw, C, sh.nq, sh.nkv, 0, 4, false);
   return hipGetLastError();
 }
 
