@@ -45,9 +45,6 @@ size_t grad_dw_one_partial_floats(int R, int C);
 hipError_t launch_grad_dw_one(const uint16_t* X, const uint16_t* G, uint16_t* dW, float* partial, int R, int C,
                               bool accumulate, hipStream_t s);
 size_t grad_dw4_partial_floats(int R, int C);
-hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
-                           const uint16_t* Xp, const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw,
-                           uint16_t* dPw, float* partial, int R, int C, bool accumulate, hipStream_t s);
 hipError_t launch_grad_dxdw4(float* dX, const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
                              const uint16_t* Wq, const uint16_t* Wk, const uint16_t* Wv, const uint16_t* Xp,
                              const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw, uint16_t* dPw, float* partial,
@@ -561,7 +558,7 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   // balanced items instead of projBackwarddW's own short-item launch. Its sum then runs over
   // other row chunks than the entry point's, so it can differ from projBackwarddW's result by the
   // fp32 summation order (one bf16 rounding step at most).
-  const bool fuse_pdw = mla::grad_dw_fused_ok(R, C);
+  const bool fuse_pdw = mla::grad_dw_fused_ok(R, C) && mla::grad_dx_fused_ok(R, C);
   if (!fuse_pdw) TRY(op_proj_dw(c, b->attn_out, b->dOut, b->dProjw, R, C, partial, false));
   TRY(op_proj_dx(c, b->dOut, b->proj_w, b->dAttn, R, C));
   if (!c.query) {
@@ -576,17 +573,12 @@ int encode(const Ctx& c, int phase, const metalllmSublayerBuffers* b, const Atte
   } else {
     split = nullptr;
   }
-  if (fuse_pdw && mla::grad_dx_fused_ok(R, C)) {
+  if (fuse_pdw) {
     // computeGradDx and the four weight gradients in one launch (dX tiles first, then the
     // weight-gradient items, which start as the dX tiles finish), then the reduction
     if (!c.query && mla::launch_grad_dxdw4(b->dX, b->X, b->dQ, b->dK, b->dV, b->q_w, b->k_w, b->v_w, b->attn_out,
                                            b->dOut, b->dQw, b->dKw, b->dVw, b->dProjw, partial, R, C,
                                            c.stream) != hipSuccess)
-      return METALLLM_ATTN_E_LAUNCH;
-  } else if (fuse_pdw) {
-    TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));
-    if (!c.query && mla::launch_grad_dw4(b->X, b->dQ, b->dK, b->dV, b->attn_out, b->dOut, b->dQw, b->dKw, b->dVw,
-                                         b->dProjw, partial, R, C, false, c.stream) != hipSuccess)
       return METALLLM_ATTN_E_LAUNCH;
   } else {
     TRY(op_grad_dx(c, b->dX, b->q_w, b->k_w, b->v_w, b->dQ, split, lo, b->dK, b->dV, R, C, false));

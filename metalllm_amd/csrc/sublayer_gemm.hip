@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(256, 2) grad_dx_kernel(float* __restrict__ dX,
 // grad_dw_reduce_kernel then adds the partials and the destination's previous value once and
 // rounds once. projBackwarddW (attention.metal:407-430, dProjw += attn_out^T.dZ) runs the same
 // kernel with one bf16 weight (grad_dw_one_shape), and the phase encoder adds it to
-// computeGradDw's launch as a fourth weight (Xp = attn_out, Gp = dZ; launch_grad_dw4).
+// computeGradDw's items as a fourth weight (Xp = attn_out, Gp = dZ; launch_grad_dxdw4).
 //
 // Operands: the tile is computed transposed, W^T = G^T . X (m = j, n = i, k = r), so each lane
 // ends with four consecutive j of one i, stored as 16-byte words of the row-major partial. Both
@@ -587,30 +587,17 @@ hipError_t launch_grad_dw(const uint16_t* X, const float* dQ, const uint16_t* dK
   return hipGetLastError();
 }
 
-// computeGradDw and projBackwarddW in one launch and one reduction (the phase encoder): dPw =
-// Xp^T . Gp (attn_out^T . dZ) as a fourth weight.
+// Partial floats of the phase encoder's four-weight form (computeGradDw with projBackwarddW's
+// dPw = Xp^T . Gp, attn_out^T . dZ, as a fourth weight; launch_grad_dxdw4).
 size_t grad_dw4_partial_floats(int R, int C) {
   const GwShape sh = grad_dw_shape(R, C, device_cus(), 3);
   return (size_t)(sh.nq + 3 * sh.nkv) * C * C;
 }
 
-hipError_t launch_grad_dw4(const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
-                           const uint16_t* Xp, const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw,
-                           uint16_t* dPw, float* partial, int R, int C, bool accumulate, hipStream_t s) {
-  const GwShape sh = grad_dw_shape(R, C, device_cus(), 3);
-  hipLaunchKernelGGL(gw_fi(C) == 192 ? grad_dw_kernel<192> : grad_dw_kernel<128>, dim3((unsigned)sh.items), dim3(256), 0,
-                     s, X, dQ, dK, dV, Xp, Gp, partial, sh);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const size_t n4 = 4 * (size_t)C * C / 4;
-  hipLaunchKernelGGL(grad_dw_reduce_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, s,
-                     partial, dQw, dKw, dVw, dPw, C, sh.nq, sh.nkv, 0, 4, accumulate);
-  return hipGetLastError();
-}
-
 // The phase encoder's computeGradDx (dX written) and four-weight computeGradDw in one launch,
-// then the reduction; the shapes of launch_grad_dx and launch_grad_dw4 (feature tiles of the same
-// width: 192 where it divides C, else 128).
+// then the reduction of the four weights; computeGradDx's tiles as launch_grad_dx's and the
+// weight-gradient items of grad_dw_shape with three bf16 weights (feature tiles of the same width:
+// 192 where it divides C, else 128).
 hipError_t launch_grad_dxdw4(float* dX, const uint16_t* X, const float* dQ, const uint16_t* dK, const uint16_t* dV,
                              const uint16_t* Wq, const uint16_t* Wk, const uint16_t* Wv, const uint16_t* Xp,
                              const uint16_t* Gp, float* dQw, uint16_t* dKw, uint16_t* dVw, uint16_t* dPw, float* partial,
